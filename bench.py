@@ -1,0 +1,273 @@
+"""Decode-step benchmark of the fused INT2/INT4 HIP path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload int4_gqa_128k]
+
+A step is one fused decode (split kernel + merge kernel) of one query token
+over the workload's packed KV cache, which is resident in HBM before timing
+starts.  Inputs are synthetic and seeded: K/V randn fp16 quantised with the
+package's own quantiser on the GPU, query randn fp16.  Several distinct copies
+of the packed cache (> 512 MB in total) are rotated across steps so the 256 MB
+Infinity Cache cannot serve repeats.
+
+Output: one JSON line.  ``value`` is packed-KV GB/s over the whole step
+(algorithmic bytes / step time); ``roofline.achieved`` is the same bytes over
+the dominant kernel's average duration, from HIP events recorded on the launch
+stream around that kernel inside the timed region.  ``cpu_baseline`` is the CPU
+oracle (a plain-C port of the reference's dequantise-then-attend path) timed on
+this host's cores over a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "kvssd-attention_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "µs/decode step + packed-KV HBM GB/s (% peak), INT4 GQA 128K tokens"
+HBM_PEAK_GBPS = 8000.0
+
+# name -> (tokens, bits, query_heads, value_scale, outlier_fraction, selector (sink, recent) or None)
+WORKLOADS = {
+    "int4_gqa_4k": (4096, 4, 32, 1.0, 0.0, None),
+    "int4_gqa_128k": (131072, 4, 32, 0.5, 0.0, None),
+    "int2_gqa_128k": (131072, 2, 32, 1.0, 0.05, None),
+    "int4_gqa8_256k_sparse": (262144, 4, 64, 1.0, 0.0, (1, 32)),
+}
+KV_HEADS, HEAD_DIM, BLOCK_TOKENS, GROUP = 8, 128, 128, 32
+
+
+def alg_bytes(n_blocks: int, bits: int) -> int:
+    """Packed K+V codes plus K+V fp16 scales read per step."""
+    per_token_head = 2 * HEAD_DIM * bits // 8 + 2 * (HEAD_DIM // GROUP) * 2
+    return n_blocks * BLOCK_TOKENS * KV_HEADS * per_token_head
+
+
+def make_cache(torch, dev, tokens, bits, qh, value_scale, outliers, seed=7):
+    from kvssd.quant import quantize_tensor
+
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    out = {}
+    for name in ("k", "v"):
+        x = torch.randn(tokens, KV_HEADS, HEAD_DIM, generator=gen, device=dev, dtype=torch.float16)
+        x = x * value_scale
+        if outliers:
+            mask = torch.rand(x.shape, generator=gen, device=dev) < outliers
+            x = torch.where(mask, x * 8, x)
+        q = quantize_tensor(x, bits, GROUP)
+        nb = tokens // BLOCK_TOKENS
+        out["p" + name] = q.packed.reshape(nb, BLOCK_TOKENS, KV_HEADS, HEAD_DIM * bits // 8)
+        out["s" + name] = q.scales.reshape(nb, BLOCK_TOKENS, KV_HEADS, HEAD_DIM // GROUP)
+        del x
+    query = torch.randn(qh, HEAD_DIM, generator=gen, device=dev, dtype=torch.float16)
+    valid = torch.full((tokens // BLOCK_TOKENS,), BLOCK_TOKENS, dtype=torch.int32, device=dev)
+    return query, out, valid
+
+
+def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 20.0):
+    """Time the CPU oracle on a bounded sample of the same workload."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    threads = O.cpu_count()
+    pk, pv = cache["pk"].cpu().numpy(), cache["pv"].cpu().numpy()
+    sk, sv = cache["sk"].cpu().numpy(), cache["sv"].cpu().numpy()
+    va = valid.cpu().numpy()
+    q = query.float().cpu().numpy()
+    ids = np.arange(pk.shape[0], dtype=np.int32) if table is None else np.asarray(table, np.int32)
+    sample = ids
+    # calibrate on a slice, then size the sample to ~budget/3 seconds per run
+    probe = ids[: max(1, min(len(ids), 16))]
+    t0 = time.perf_counter()
+    O.attention(q, pk, pv, sk, sv, va, bits, GROUP, 1 / math.sqrt(HEAD_DIM), block_table=probe, threads=threads)
+    per_block = (time.perf_counter() - t0) / len(probe)
+    n = int(max(1, min(len(ids), (budget_s / 3) / max(per_block, 1e-9))))
+    sample = ids[:n]
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.attention(q, pk, pv, sk, sv, va, bits, GROUP, 1 / math.sqrt(HEAD_DIM), block_table=sample, threads=threads)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    nbytes = alg_bytes(len(sample), bits)
+    return {
+        "value": round(nbytes / t / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{len(sample)} of {len(ids)} blocks of the same packed batch, median of 3 runs "
+        f"({t * 1e3:.1f} ms each; full step extrapolates to {t * len(ids) / len(sample) * 1e3:.1f} ms)",
+        "ms_per_full_step": round(t * len(ids) / len(sample) * 1e3, 3),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="int4_gqa_128k", choices=sorted(WORKLOADS))
+    ap.add_argument("--kernel", default="auto", choices=["auto", "general", "mfma"])
+    ap.add_argument("--copies", type=int, default=0, help="distinct KV copies rotated across steps (0 = auto)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(
+            "bench.py measures one GPU only: this build has no multi-GPU path "
+            "(the decode shards by kv head or by token range across GPUs; see DESIGN.md)",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from kvssd import _native
+    from kvssd.backends import PackedBatch
+    from kvssd.backends.hip import HipAttentionBackend
+    from kvssd.selectors import RecentSinkBlocks
+
+    dev = torch.device("cuda", 0)
+    tokens, bits, qh, vscale, outl, sel = WORKLOADS[args.workload]
+    query, cache, valid = make_cache(torch, dev, tokens, bits, qh, vscale, outl)
+    nb = tokens // BLOCK_TOKENS
+    table = None
+    if sel is not None:
+        table = RecentSinkBlocks(*sel).select(list(range(nb)))
+    n_read = nb if table is None else len(table)
+    nbytes = alg_bytes(n_read, bits)
+    cache_bytes = sum(t.numel() * t.element_size() for t in cache.values())
+    copies = args.copies or max(1, min(16, math.ceil(1.2e9 / max(cache_bytes, 1))))
+    if table is not None:
+        copies = args.copies or 8
+    batches = [PackedBatch(cache["pk"], cache["pv"], cache["sk"], cache["sv"], valid, bits, GROUP)]
+    for _ in range(copies - 1):
+        batches.append(PackedBatch(*(cache[k].clone() for k in ("pk", "pv", "sk", "sv")), valid, bits, GROUP))
+
+    backend = HipAttentionBackend(args.kernel)
+    scale = 1 / math.sqrt(HEAD_DIM)
+    lib = _native.load()
+    tab = None
+    if table is not None:
+        tab = torch.tensor(table, dtype=torch.int32, device=dev)
+    desc = backend.describe(query, batches[0], scale, 0 if tab is None else tab.numel())
+    need = ctypes.c_size_t(0)
+    _native.check(lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(need)), "workspace")
+    kern = ctypes.c_int(0)
+    _native.check(lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(kern)), "kernel")
+    kernel_name = _native.KERNEL_NAMES[kern.value]
+    work = torch.empty(int(need.value), dtype=torch.uint8, device=dev)
+    out = torch.empty(qh, HEAD_DIM, dtype=torch.float32, device=dev)
+    lse = torch.empty(qh, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = _native.stream_handle(stream)
+    tab_ptr = None if tab is None else tab.data_ptr()
+
+    def step(i: int, ev=None):
+        b = batches[i % copies]
+        if ev is not None:
+            ev[0].record(stream)
+        rc = lib.kvssd_hip_decode_partials(
+            ctypes.byref(desc), query.data_ptr(), b.packed_k.data_ptr(), b.packed_v.data_ptr(),
+            b.scales_k.data_ptr(), b.scales_v.data_ptr(), b.valid_tokens.data_ptr(), tab_ptr,
+            work.data_ptr(), work.numel(), sh,
+        )
+        if ev is not None:
+            ev[1].record(stream)
+        rc2 = lib.kvssd_hip_decode_merge(ctypes.byref(desc), work.data_ptr(), work.numel(), out.data_ptr(), lse.data_ptr(), sh)
+        if rc or rc2:
+            _native.check(rc or rc2, "decode")
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i, evs[i])
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    total_ms = evs[0][0].elapsed_time(end)
+    kern_ms = [a.elapsed_time(b) for a, b in evs]
+    step_ms = [evs[i][0].elapsed_time(evs[i + 1][0]) for i in range(args.steps - 1)] + [evs[-1][0].elapsed_time(end)]
+    ms_per_step = total_ms / args.steps
+    kern_avg = sum(kern_ms) / len(kern_ms)
+
+    def pct(xs, p):
+        s = sorted(xs)
+        return s[min(len(s) - 1, int(p * len(s)))]
+
+    gbps = nbytes / (ms_per_step * 1e-3) / 1e9
+    achieved = nbytes / (kern_avg * 1e-3) / 1e9
+    # quick numerical sanity on the last step's output against the portable path
+    ok = bool(torch.isfinite(out).all().item())
+
+    traffic = None
+    tfile = ROOT / "profiles" / f"traffic_{args.workload}_{kernel_name}.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "us_per_step": round(ms_per_step * 1e3, 2),
+        "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16" if kernel_name == "mfma" else "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": args.workload,
+            "tokens": tokens,
+            "bits": bits,
+            "kv_heads": KV_HEADS,
+            "query_heads": qh,
+            "head_dim": HEAD_DIM,
+            "block_tokens": BLOCK_TOKENS,
+            "group_size": GROUP,
+            "blocks_read": n_read,
+            "selector": "all" if sel is None else f"recent_sink{sel}",
+            "kernel": kernel_name,
+            "kv_copies_rotated": copies,
+            "alg_bytes_per_step": nbytes,
+        },
+        "step_us": {"p10": round(pct(step_ms, 0.1) * 1e3, 2), "p50": round(pct(step_ms, 0.5) * 1e3, 2), "p90": round(pct(step_ms, 0.9) * 1e3, 2)},
+        "kernel_us": {"avg": round(kern_avg * 1e3, 2), "p50": round(pct(kern_ms, 0.5) * 1e3, 2)},
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "kernel": f"decode_{kernel_name}",
+        },
+        "host_wall_ms_per_step": round(wall / args.steps * 1e3, 4),
+        "finite": ok,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch, query, {k: batches[0].__dict__[n] for k, n in (("pk", "packed_k"), ("pv", "packed_v"), ("sk", "scales_k"), ("sv", "scales_v"))}, valid, bits, table)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

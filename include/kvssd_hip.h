@@ -1,0 +1,148 @@
+/*
+ * kvssd_hip.h: C ABI of libkvssd_hip.so, the MI355X (gfx950) fused INT2/INT4
+ * dequant + decode-attention library.
+ *
+ * This ABI replaces the reference's pybind/torch extension kvssd._C
+ * (csrc/bindings.cpp:16-45, csrc/fused_decode.cu:92-143).  It uses plain C
+ * types only: device pointers, sizes and a hipStream_t passed as void*.
+ *
+ * Conventions
+ *   - Every call returns 0 on success.  A negative value is an argument error:
+ *     the message is available from kvssd_hip_last_error() and mirrors the
+ *     reference's check (the Python layer raises ValueError).  A positive value
+ *     is a hipError_t from the runtime (the Python layer raises RuntimeError).
+ *   - The caller allocates every buffer, including the workspace.  The library
+ *     never allocates or frees device memory.
+ *   - Every launch is asynchronous on `stream` (a hipStream_t; NULL means the
+ *     null stream); no call synchronises the host.
+ *   - The library keeps no per-call state; the only global state is a
+ *     thread-local error string and a per-device property cache filled once.
+ *     Calls are reentrant from any host thread.
+ */
+#ifndef KVSSD_HIP_H
+#define KVSSD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KVSSD_HIP_ABI_VERSION 1
+
+/* Query element types accepted by kvssd_hip_fused_decode (the reference
+ * dispatches fp32/fp64/fp16/bf16 queries: csrc/fused_decode.cu:131-133). */
+enum kvssd_dtype {
+  KVSSD_DTYPE_F16 = 0,
+  KVSSD_DTYPE_BF16 = 1,
+  KVSSD_DTYPE_F32 = 2,
+  KVSSD_DTYPE_F64 = 3
+};
+
+/* Kernel selection for kvssd_hip_fused_decode. */
+enum kvssd_kernel {
+  KVSSD_KERNEL_AUTO = 0,    /* fastest kernel that supports the shape */
+  KVSSD_KERNEL_GENERAL = 1, /* any shape the reference accepts */
+  KVSSD_KERNEL_MFMA = 2     /* matrix-core kernel: head_dim 128, group_size 32 */
+};
+
+/* Shape of one decode call.  The packed arrays follow the reference's
+ * PackedBatch layout (src/kvssd/backends/base.py:19-27):
+ *   packed_k, packed_v  uint8   [num_blocks, block_tokens, kv_heads, head_dim*bits/8]
+ *   scales_k, scales_v  float16 [num_blocks, block_tokens, kv_heads, head_dim/group_size]
+ *   valid_tokens        int32   [num_blocks]
+ * all C-contiguous.  When block_table is not NULL it lists num_selected block
+ * ids (int32, each in [0, num_blocks)) and the call attends over those blocks
+ * in table order; with NULL it attends over blocks 0..num_blocks-1. */
+typedef struct kvssd_decode_desc {
+  int32_t query_heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t num_blocks;
+  int32_t block_tokens;
+  int32_t bits;
+  int32_t group_size;
+  int32_t query_dtype;  /* enum kvssd_dtype */
+  int32_t num_selected; /* entries in block_table; ignored when it is NULL */
+  int32_t kernel;       /* enum kvssd_kernel */
+  double sm_scale;
+} kvssd_decode_desc;
+
+/* ABI version of the loaded library (KVSSD_HIP_ABI_VERSION). */
+int kvssd_hip_abi_version(void);
+
+/* 1 when `device` is a gfx950 GPU this library has code for, else 0, with the
+ * reason written to `why` (NUL-terminated, at most why_len bytes).  Backs
+ * HipAttentionBackend.probe(); replaces the device check of
+ * src/kvssd/backends/cuda.py:20-29. */
+int kvssd_hip_device_ok(int device, char* why, size_t why_len);
+
+/* Device workspace bytes kvssd_hip_fused_decode needs for `desc`. */
+int kvssd_hip_decode_workspace_bytes(const kvssd_decode_desc* desc, size_t* bytes);
+
+/* Which kernel kvssd_hip_fused_decode would run for `desc` (enum kvssd_kernel;
+ * never KVSSD_KERNEL_AUTO). */
+int kvssd_hip_decode_kernel(const kvssd_decode_desc* desc, int* kernel);
+
+/* Fused decode attention over a packed batch: out fp32 [query_heads, head_dim]
+ * (softmax-normalised), lse fp32 [query_heads] (natural-log log-sum-exp of the
+ * scaled scores).  Replaces kvssd._C.fused_decode (csrc/bindings.cpp:16-41,
+ * csrc/fused_decode.cu:92-143) with the semantics of
+ * ReferenceAttentionBackend.run (src/kvssd/backends/reference.py:22-50):
+ * valid_tokens[b] is clamped to [0, block_tokens]; with no valid token at all
+ * out is 0 and lse is -inf.  `query` holds query_heads*head_dim elements of
+ * query_dtype. */
+int kvssd_hip_fused_decode(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k,
+                           const uint8_t* packed_v, const uint16_t* scales_k, const uint16_t* scales_v,
+                           const int32_t* valid_tokens, const int32_t* block_table, float* out, float* lse,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Phase 1 of kvssd_hip_fused_decode alone: every split writes its
+ * unnormalised partial (O, running max, running sum) into `workspace`.
+ * kvssd_hip_decode_merge turns them into (out, lse).  Same arguments and checks
+ * as kvssd_hip_fused_decode; no reference counterpart (the reference kernel is
+ * one pass, csrc/fused_decode.cu:12-90).  Lets a caller time or overlap the
+ * two phases separately. */
+int kvssd_hip_decode_partials(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k,
+                              const uint8_t* packed_v, const uint16_t* scales_k, const uint16_t* scales_v,
+                              const int32_t* valid_tokens, const int32_t* block_table, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* Phase 2: merge the split partials left in `workspace` by
+ * kvssd_hip_decode_partials for the same `desc` into out / lse. */
+int kvssd_hip_decode_merge(const kvssd_decode_desc* desc, const void* workspace, size_t workspace_bytes, float* out,
+                           float* lse, void* stream);
+
+/* Running exact merge of normalised attention chunks, in place:
+ *   L = logaddexp(acc_lse, lse); acc_out = acc_out e^(acc_lse-L) + out e^(lse-L)
+ * over `rows` rows of `dim` fp32 values.  Replaces merge_attention_chunks
+ * (src/kvssd/attention.py:287-298) in the pipeline's chunk loop
+ * (src/kvssd/pipeline.py:147-153).  A chunk with lse = -inf adds nothing. */
+int kvssd_hip_merge_chunks(int rows, int dim, float* acc_out, float* acc_lse, const float* out, const float* lse,
+                           void* stream);
+
+/* Unsigned codes of `n_bytes` packed bytes (8/bits codes per byte, low bits
+ * first), unpacked by the same in-register routine the fused kernels use.
+ * Bit-exact twin of unpack_codes (src/kvssd/quant.py:66-72). */
+int kvssd_hip_unpack_codes(const uint8_t* packed, int bits, int64_t n_bytes, uint8_t* codes, void* stream);
+
+/* fp32 (code - mid) * scale for `rows` rows of `head_dim` elements
+ * (packed [rows, head_dim*bits/8], scales [rows, head_dim/group_size]).
+ * Twin of dequantize_tensor (src/kvssd/quant.py:94-99); exact. */
+int kvssd_hip_dequantize(const uint8_t* packed, const uint16_t* scales, int64_t rows, int head_dim, int bits,
+                         int group_size, float* out, void* stream);
+
+/* hipMemcpyAsync host->device of `bytes` bytes on `stream`; `src` should be
+ * page-locked for the copy to be asynchronous.  The staging copy of
+ * KVSSDPipeline._stage (src/kvssd/pipeline.py:110-114). */
+int kvssd_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes, void* stream);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* kvssd_hip_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KVSSD_HIP_H */

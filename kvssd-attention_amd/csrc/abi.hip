@@ -1,0 +1,251 @@
+// extern "C" entry points of libkvssd_hip.so (declared in include/kvssd_hip.h).
+//
+// Argument checks mirror the reference's (csrc/bindings.cpp:26-38,
+// csrc/fused_decode.cu:117-121, src/kvssd/backends/base.py:29-55) so callers
+// see the same failures; they run on the host before any launch, and every
+// launch's grid is derived from the validated shape.
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "decode.hpp"
+
+namespace kvssd {
+
+namespace {
+thread_local std::string g_last_error;
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_props_once[kMaxDevices];
+int g_is_gfx950[kMaxDevices];
+std::string g_arch[kMaxDevices];
+
+}  // namespace
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+
+int arg_error(const std::string& msg) {
+  set_error(msg);
+  return kArgError;
+}
+
+int hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return 0;
+  set_error(std::string(what) + ": " + hipGetErrorString(err));
+  return static_cast<int>(err);
+}
+
+namespace {
+
+int validate(const kvssd_decode_desc* d, int* units) {
+  if (d == nullptr) return arg_error("descriptor is NULL");
+  if (d->query_heads <= 0 || d->head_dim <= 0) return arg_error("query must be [query_heads, head_dim]");
+  if (d->num_blocks <= 0 || d->block_tokens <= 0 || d->kv_heads <= 0)
+    return arg_error("packed KV must match [blocks,tokens,kv_heads,packed_dim]");
+  if (d->bits != 2 && d->bits != 4) return arg_error("bits must be 2 or 4");
+  if (d->group_size <= 0 || d->head_dim % d->group_size) return arg_error("group_size must divide head_dim");
+  if ((d->head_dim * d->bits) % 8) return arg_error("packed dimension does not match query head dimension");
+  if (d->group_size % (8 / d->bits)) return arg_error("group_size must be positive and pack-aligned");
+  if (d->query_heads % d->kv_heads) return arg_error("query heads must be divisible by KV heads");
+  if (d->head_dim > 256) return arg_error("head_dim must be <= 256");
+  if (d->query_dtype < KVSSD_DTYPE_F16 || d->query_dtype > KVSSD_DTYPE_F64) return arg_error("unsupported query dtype");
+  if (d->kernel < KVSSD_KERNEL_AUTO || d->kernel > KVSSD_KERNEL_MFMA) return arg_error("unknown kernel selector");
+  *units = d->num_blocks;
+  return 0;
+}
+
+int choose_kernel(const kvssd_decode_desc& d, int* kernel) {
+  std::string why;
+  const bool mfma = mfma_supported(d, &why);
+  if (d.kernel == KVSSD_KERNEL_MFMA) {
+    if (!mfma) return arg_error("matrix-core kernel does not support this shape: " + why);
+    *kernel = KVSSD_KERNEL_MFMA;
+  } else if (d.kernel == KVSSD_KERNEL_GENERAL) {
+    *kernel = KVSSD_KERNEL_GENERAL;
+  } else {
+    *kernel = mfma ? KVSSD_KERNEL_MFMA : KVSSD_KERNEL_GENERAL;
+  }
+  return 0;
+}
+
+int plan_splits(const kvssd_decode_desc& d, int units, int kernel, int* splits) {
+  if (kernel == KVSSD_KERNEL_MFMA) {
+    *splits = plan_mfma(d, units).splits;
+  } else {
+    *splits = plan_general(d, units).splits;
+  }
+  return 0;
+}
+
+int units_of(const kvssd_decode_desc* d, const int32_t* table, int* units) {
+  if (table != nullptr) {
+    if (d->num_selected <= 0) return arg_error("at least one block is required");
+    *units = d->num_selected;
+  }
+  return 0;
+}
+
+// Validation, unit count, kernel choice and split plan shared by the phases.
+int prepare(const kvssd_decode_desc* desc, const int32_t* table, void* workspace, size_t workspace_bytes, int* units,
+            int* kernel, int* splits) {
+  if (int rc = validate(desc, units)) return rc;
+  if (int rc = units_of(desc, table, units)) return rc;
+  if (int rc = choose_kernel(*desc, kernel)) return rc;
+  plan_splits(*desc, *units, *kernel, splits);
+  const size_t need = split_partial_bytes(*splits, desc->query_heads, desc->head_dim);
+  if (workspace == nullptr || workspace_bytes < need)
+    return arg_error("workspace too small: need " + std::to_string(need) + " bytes");
+  return 0;
+}
+
+}  // namespace
+}  // namespace kvssd
+
+using namespace kvssd;
+
+extern "C" {
+
+__attribute__((visibility("default"))) int kvssd_hip_abi_version(void) { return KVSSD_HIP_ABI_VERSION; }
+
+__attribute__((visibility("default"))) const char* kvssd_hip_last_error(void) { return g_last_error.c_str(); }
+
+__attribute__((visibility("default"))) int kvssd_hip_device_ok(int device, char* why, size_t why_len) {
+  auto say = [&](const std::string& s) {
+    if (why != nullptr && why_len > 0) {
+      std::snprintf(why, why_len, "%s", s.c_str());
+    }
+  };
+  int count = 0;
+  hipError_t err = hipGetDeviceCount(&count);
+  if (err != hipSuccess || count <= 0) {
+    say("no HIP device is visible");
+    return 0;
+  }
+  if (device < 0 || device >= count || device >= kMaxDevices) {
+    say("HIP device index out of range");
+    return 0;
+  }
+  std::call_once(g_props_once[device], [device] {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
+      g_arch[device] = prop.gcnArchName;
+      g_is_gfx950[device] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    } else {
+      g_arch[device] = "unknown";
+      g_is_gfx950[device] = 0;
+    }
+  });
+  if (!g_is_gfx950[device]) {
+    say("libkvssd_hip is built for gfx950 (MI355X); device " + std::to_string(device) + " is " + g_arch[device]);
+    return 0;
+  }
+  say("gfx950 HIP kernels available");
+  return 1;
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_decode_kernel(const kvssd_decode_desc* desc, int* kernel) {
+  int units = 0;
+  if (int rc = validate(desc, &units)) return rc;
+  if (kernel == nullptr) return arg_error("kernel output pointer is NULL");
+  return choose_kernel(*desc, kernel);
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_decode_workspace_bytes(const kvssd_decode_desc* desc,
+                                                                            size_t* bytes) {
+  int units = 0;
+  if (int rc = validate(desc, &units)) return rc;
+  if (bytes == nullptr) return arg_error("bytes output pointer is NULL");
+  if (desc->num_selected > 0) units = desc->num_selected;
+  int kernel = 0;
+  if (int rc = choose_kernel(*desc, &kernel)) return rc;
+  int splits = 0;
+  plan_splits(*desc, units, kernel, &splits);
+  *bytes = split_partial_bytes(splits, desc->query_heads, desc->head_dim);
+  return 0;
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_decode_partials(
+    const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
+    const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens, const int32_t* block_table,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  int units = 0, kernel = 0, splits = 0;
+  if (int rc = prepare(desc, block_table, workspace, workspace_bytes, &units, &kernel, &splits)) return rc;
+  if (!query || !packed_k || !packed_v || !scales_k || !scales_v || !valid_tokens)
+    return arg_error("a required buffer pointer is NULL");
+  DecodeArgs a{};
+  a.desc = *desc;
+  a.query = query;
+  a.packed_k = packed_k;
+  a.packed_v = packed_v;
+  a.scales_k = scales_k;
+  a.scales_v = scales_v;
+  a.valid = valid_tokens;
+  a.table = block_table;
+  a.units = units;
+  a.stream = static_cast<hipStream_t>(stream);
+  SplitPartials parts = carve_partials(workspace, splits, desc->query_heads, desc->head_dim);
+  if (kernel == KVSSD_KERNEL_MFMA) return launch_mfma(a, plan_mfma(*desc, units), parts);
+  return launch_general(a, plan_general(*desc, units), parts);
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_decode_merge(const kvssd_decode_desc* desc,
+                                                                  const void* workspace, size_t workspace_bytes,
+                                                                  float* out, float* lse, void* stream) {
+  int units = 0, kernel = 0, splits = 0;
+  // the table pointer only matters for its NULL-ness: units come from the descriptor
+  const int32_t* marker = (desc && desc->num_selected > 0) ? reinterpret_cast<const int32_t*>(1) : nullptr;
+  if (int rc = prepare(desc, marker, const_cast<void*>(workspace), workspace_bytes, &units, &kernel, &splits))
+    return rc;
+  if (!out || !lse) return arg_error("a required buffer pointer is NULL");
+  SplitPartials parts = carve_partials(const_cast<void*>(workspace), splits, desc->query_heads, desc->head_dim);
+  return launch_merge_splits(parts, splits, desc->query_heads, desc->head_dim, out, lse,
+                             static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_fused_decode(
+    const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
+    const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens, const int32_t* block_table,
+    float* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!out || !lse) return arg_error("a required buffer pointer is NULL");
+  if (int rc = kvssd_hip_decode_partials(desc, query, packed_k, packed_v, scales_k, scales_v, valid_tokens,
+                                         block_table, workspace, workspace_bytes, stream))
+    return rc;
+  return kvssd_hip_decode_merge(desc, workspace, workspace_bytes, out, lse, stream);
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_merge_chunks(int rows, int dim, float* acc_out, float* acc_lse,
+                                                                  const float* out, const float* lse, void* stream) {
+  if (rows <= 0 || dim <= 0) return arg_error("merge needs positive rows and dim");
+  if (!acc_out || !acc_lse || !out || !lse) return arg_error("a required buffer pointer is NULL");
+  return launch_merge_chunks(rows, dim, acc_out, acc_lse, out, lse, static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_unpack_codes(const uint8_t* packed, int bits, int64_t n_bytes,
+                                                                  uint8_t* codes, void* stream) {
+  if (bits != 2 && bits != 4) return arg_error("bits must be 2 or 4");
+  if (n_bytes < 0) return arg_error("n_bytes must be non-negative");
+  if (n_bytes > 0 && (!packed || !codes)) return arg_error("a required buffer pointer is NULL");
+  return launch_unpack_codes(packed, bits, n_bytes, codes, static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_dequantize(const uint8_t* packed, const uint16_t* scales,
+                                                                int64_t rows, int head_dim, int bits, int group_size,
+                                                                float* out, void* stream) {
+  if (bits != 2 && bits != 4) return arg_error("bits must be 2 or 4");
+  if (rows < 0 || head_dim <= 0) return arg_error("rows must be >= 0 and head_dim positive");
+  if (group_size <= 0 || head_dim % group_size) return arg_error("group_size must divide head_dim");
+  if ((head_dim * bits) % 8) return arg_error("packed dimension does not match query head dimension");
+  if (rows > 0 && (!packed || !scales || !out)) return arg_error("a required buffer pointer is NULL");
+  return launch_dequantize(packed, scales, rows, head_dim, bits, group_size, out, static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes,
+                                                                      void* stream) {
+  if (bytes == 0) return 0;
+  if (!dst || !src) return arg_error("a required buffer pointer is NULL");
+  return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream)),
+                    "hipMemcpyAsync");
+}
+
+}  // extern "C"

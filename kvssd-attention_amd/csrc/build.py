@@ -1,0 +1,88 @@
+"""Build libkvssd_hip.so for gfx950 with hipcc (no CMake, no torch extension).
+
+    python kvssd-attention_amd/csrc/build.py [--jobs N] [--verbose]
+
+Each .hip file compiles to an object in csrc/_build/, then the objects link into
+kvssd-attention_amd/kvssd/libkvssd_hip.so, which the kvssd package loads with
+ctypes after ``import torch`` so it shares torch's HIP runtime
+(libamdhip64.so.7).
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+PKG = HERE.parent / "kvssd"
+OUT = PKG / "libkvssd_hip.so"
+BUILD = HERE / "_build"
+SOURCES = ["abi.hip", "decode_general.hip", "decode_mfma.hip", "merge.hip", "codec.hip"]
+ARCH = "gfx950"
+
+COMMON = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-fvisibility=hidden",
+    "-mcode-object-version=5",
+    # packed fp32 VALU forms stay off: hipcc may not emit v_pk_{add,mul,fma}_f32
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-result",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(path).exists():
+        raise RuntimeError("hipcc not found; install ROCm or put /opt/rocm/bin on PATH")
+    return path
+
+
+def _run(cmd: list[str], verbose: bool) -> None:
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "'-packed-fp32-ops' is not a recognized feature"
+    err = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+
+
+def build(jobs: int = 0, verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    cc = hipcc()
+    objs = [BUILD / (Path(s).stem + ".o") for s in SOURCES]
+    cmds = [[cc, *COMMON, "-c", str(HERE / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
+    workers = jobs or min(len(cmds), os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for fut in [pool.submit(_run, c, verbose) for c in cmds]:
+            fut.result()
+    tmp = OUT.with_suffix(".so.tmp")
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__)
+    ap.add_argument("--jobs", type=int, default=0)
+    ap.add_argument("--verbose", action="store_true")
+    args = ap.parse_args()
+    print(build(args.jobs, args.verbose))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,131 @@
+// Shared host/device helpers of libkvssd_hip.so (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/kvssd_hip.h"
+
+namespace kvssd {
+
+// ---------------------------------------------------------------- errors ---
+
+// Argument errors are negative, runtime errors are the positive hipError_t.
+constexpr int kArgError = -1;
+
+void set_error(const std::string& msg);
+int arg_error(const std::string& msg);
+int hip_status(hipError_t err, const char* what);
+
+// ------------------------------------------------------------- constants ---
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kWave = 64;
+
+// Workspace of a split decode: per (split, query head) an unnormalised fp32
+// output row O[D] plus (m, l), m the running max in log2 units and l the sum of
+// 2^(s - m) over the split's tokens.
+struct SplitPartials {
+  float* o;   // [splits][query_heads][head_dim]
+  float* ml;  // [splits][query_heads][2]
+};
+
+inline size_t split_partial_bytes(int splits, int query_heads, int head_dim) {
+  size_t rows = static_cast<size_t>(splits) * query_heads;
+  size_t o = rows * head_dim * sizeof(float);
+  o = (o + 255) & ~static_cast<size_t>(255);
+  return o + rows * 2 * sizeof(float);
+}
+
+inline SplitPartials carve_partials(void* ws, int splits, int query_heads, int head_dim) {
+  size_t rows = static_cast<size_t>(splits) * query_heads;
+  size_t o = rows * head_dim * sizeof(float);
+  o = (o + 255) & ~static_cast<size_t>(255);
+  auto* base = static_cast<char*>(ws);
+  return SplitPartials{reinterpret_cast<float*>(base), reinterpret_cast<float*>(base + o)};
+}
+
+// ------------------------------------------------------------ device side ---
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+template <typename QT>
+__device__ __forceinline__ float load_query(const void* q, int index);
+
+template <>
+__device__ __forceinline__ float load_query<_Float16>(const void* q, int index) {
+  return static_cast<float>(static_cast<const _Float16*>(q)[index]);
+}
+template <>
+__device__ __forceinline__ float load_query<uint16_t>(const void* q, int index) {  // bfloat16 bits
+  uint32_t bits = static_cast<uint32_t>(static_cast<const uint16_t*>(q)[index]) << 16;
+  return __builtin_bit_cast(float, bits);
+}
+template <>
+__device__ __forceinline__ float load_query<float>(const void* q, int index) {
+  return static_cast<const float*>(q)[index];
+}
+template <>
+__device__ __forceinline__ float load_query<double>(const void* q, int index) {
+  return static_cast<float>(static_cast<const double*>(q)[index]);
+}
+
+__device__ __forceinline__ int clamp_valid(int v, int block_tokens) {
+  return v < 0 ? 0 : (v > block_tokens ? block_tokens : v);
+}
+
+// Wave-wide reductions over the 64 lanes (result in every lane).
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// --- in-register unpack of packed codes into fp16 pairs (magic numbers) ---
+//
+// A code c sits in the mantissa of an fp16 whose exponent field is that of
+// 1.0 (0x3C00):
+//   INT4: bits 6..9  -> value 1 + c/16, so c - 8 = 16 * (value - 1.5)
+//   INT2: bits 8..9  -> value 1 + c/4,  so c - 2 =  4 * (value - 1.5)
+// i.e. (c - mid) = 2^bits * (value - 1.5) for both widths.  Each output word
+// holds two fp16 lanes (lo, hi).  One AND-OR plus at most one shift per word.
+//
+// INT4, x holds nibbles n0..n7 (n_i = bits 4i..4i+3, i.e. dims d0..d7 of a
+// packed row, low bits first):
+//   w0 = (n0, n4), w1 = (n1, n5), w2 = (n2, n6), w3 = (n3, n7).
+// INT2, x holds codes c0..c15 (bits 2i..2i+1):
+//   w_j = (c_j, c_{j+8}) for j = 0..7.
+constexpr uint32_t kF16One2 = 0x3C003C00u;
+
+__device__ __forceinline__ void unpack_int4_f16(uint32_t x, uint32_t w[4]) {
+  constexpr uint32_t m = 0x03C003C0u;
+  w[0] = ((x << 6) & m) | kF16One2;
+  w[1] = ((x << 2) & m) | kF16One2;
+  w[2] = ((x >> 2) & m) | kF16One2;
+  w[3] = ((x >> 6) & m) | kF16One2;
+}
+
+__device__ __forceinline__ void unpack_int2_f16(uint32_t x, uint32_t w[8]) {
+  constexpr uint32_t m = 0x03000300u;
+  w[0] = ((x << 8) & m) | kF16One2;
+  w[1] = ((x << 6) & m) | kF16One2;
+  w[2] = ((x << 4) & m) | kF16One2;
+  w[3] = ((x << 2) & m) | kF16One2;
+  w[4] = (x & m) | kF16One2;
+  w[5] = ((x >> 2) & m) | kF16One2;
+  w[6] = ((x >> 4) & m) | kF16One2;
+  w[7] = ((x >> 6) & m) | kF16One2;
+}
+
+}  // namespace kvssd

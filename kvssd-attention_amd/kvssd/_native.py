@@ -1,0 +1,131 @@
+"""ctypes binding of libkvssd_hip.so (the C ABI in include/kvssd_hip.h).
+
+This replaces the reference's pybind/torch extension ``kvssd._C``
+(csrc/bindings.cpp:16-45).  The library is loaded after ``import torch`` so the
+dynamic loader resolves its ``libamdhip64.so.7`` dependency to the HIP runtime
+torch already mapped: device pointers and streams from torch are then valid in
+the library.  Loading fails loudly; nothing falls back to another path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede the library load; see module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "libkvssd_hip.so"
+ABI_VERSION = 1
+
+DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3
+KERNEL_AUTO, KERNEL_GENERAL, KERNEL_MFMA = 0, 1, 2
+KERNEL_NAMES = {KERNEL_AUTO: "auto", KERNEL_GENERAL: "general", KERNEL_MFMA: "mfma"}
+
+QUERY_DTYPES = {
+    torch.float16: DTYPE_F16,
+    torch.bfloat16: DTYPE_BF16,
+    torch.float32: DTYPE_F32,
+    torch.float64: DTYPE_F64,
+}
+
+
+class DecodeDesc(ctypes.Structure):
+    _fields_ = [
+        ("query_heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("num_blocks", ctypes.c_int32),
+        ("block_tokens", ctypes.c_int32),
+        ("bits", ctypes.c_int32),
+        ("group_size", ctypes.c_int32),
+        ("query_dtype", ctypes.c_int32),
+        ("num_selected", ctypes.c_int32),
+        ("kernel", ctypes.c_int32),
+        ("sm_scale", ctypes.c_double),
+    ]
+
+
+# (name, restype, argtypes) for every entry point in include/kvssd_hip.h
+_VP, _SZ, _I, _I64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int64
+SIGNATURES = {
+    "kvssd_hip_abi_version": (_I, []),
+    "kvssd_hip_device_ok": (_I, [_I, ctypes.c_char_p, _SZ]),
+    "kvssd_hip_decode_workspace_bytes": (_I, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(_SZ)]),
+    "kvssd_hip_decode_kernel": (_I, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(_I)]),
+    "kvssd_hip_fused_decode": (_I, [ctypes.POINTER(DecodeDesc)] + [_VP] * 10 + [_SZ, _VP]),
+    "kvssd_hip_decode_partials": (_I, [ctypes.POINTER(DecodeDesc)] + [_VP] * 8 + [_SZ, _VP]),
+    "kvssd_hip_decode_merge": (_I, [ctypes.POINTER(DecodeDesc), _VP, _SZ, _VP, _VP, _VP]),
+    "kvssd_hip_merge_chunks": (_I, [_I, _I, _VP, _VP, _VP, _VP, _VP]),
+    "kvssd_hip_unpack_codes": (_I, [_VP, _I, _I64, _VP, _VP]),
+    "kvssd_hip_dequantize": (_I, [_VP, _VP, _I64, _I, _I, _I, _VP, _VP]),
+    "kvssd_hip_memcpy_h2d_async": (_I, [_VP, _VP, _SZ, _VP]),
+    "kvssd_hip_last_error": (ctypes.c_char_p, []),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_load_error: str | None = None
+
+
+class NativeError(RuntimeError):
+    """A runtime failure reported by libkvssd_hip (positive status)."""
+
+
+def load() -> ctypes.CDLL:
+    """Load and type the library once; raises RuntimeError when it is absent or stale."""
+    global _lib, _load_error
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            _load_error = f"{LIB_PATH.name} is not built; run python kvssd-attention_amd/csrc/build.py"
+            raise RuntimeError(_load_error)
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as exc:
+            _load_error = f"cannot load {LIB_PATH}: {exc}"
+            raise RuntimeError(_load_error) from exc
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        version = lib.kvssd_hip_abi_version()
+        if version != ABI_VERSION:
+            _load_error = f"{LIB_PATH.name} ABI {version} != expected {ABI_VERSION}; rebuild it"
+            raise RuntimeError(_load_error)
+        _lib = lib
+        return lib
+
+
+def available() -> tuple[bool, str]:
+    try:
+        load()
+        return True, "libkvssd_hip loaded"
+    except RuntimeError as exc:
+        return False, str(exc)
+
+
+def last_error() -> str:
+    msg = load().kvssd_hip_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    """Map a status to the reference's exception types (ValueError / RuntimeError)."""
+    if rc == 0:
+        return
+    msg = last_error() or what
+    if rc < 0:
+        raise ValueError(msg)
+    raise NativeError(f"{what} failed with hipError {rc}: {msg}")
+
+
+def device_ok(index: int) -> tuple[bool, str]:
+    buf = ctypes.create_string_buffer(256)
+    ok = load().kvssd_hip_device_ok(index, buf, len(buf))
+    return bool(ok), buf.value.decode()
+
+
+def stream_handle(stream: torch.cuda.Stream | None) -> int:
+    return 0 if stream is None else int(stream.cuda_stream)

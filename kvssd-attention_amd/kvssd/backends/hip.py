@@ -1,0 +1,189 @@
+"""``hip`` attention backend: the fused INT2/INT4 decode kernels on gfx950.
+
+Takes over the role of the reference's CudaExtensionBackend
+(src/kvssd/backends/cuda.py:17-48), calling libkvssd_hip.so through its C ABI
+(include/kvssd_hip.h) instead of the torch extension ``kvssd._C``.
+
+* ``probe`` reports available only on a ROCm build of torch with a visible
+  gfx950 device and the library loaded (checked once per device).
+* ``run`` validates the batch exactly like the reference, checks dtypes as
+  csrc/bindings.cpp:34-36 does, allocates out / lse / workspace with torch on
+  the query's device and launches on torch's current stream.  It never
+  synchronises the host and never reads device tensors back (no
+  ``.tolist()`` as in src/kvssd/backends/triton.py:170).
+* There is no fallback: a missing library or device raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Sequence
+
+import torch
+
+from .. import _native
+from .base import BackendAvailability, PackedBatch
+
+_device_state: dict[int, tuple[bool, str]] = {}
+
+
+def _index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+class HipAttentionBackend:
+    name = "hip"
+
+    def __init__(self, kernel: str = "auto"):
+        names = {v: k for k, v in _native.KERNEL_NAMES.items()}
+        if kernel not in names:
+            raise ValueError(f"unknown hip kernel '{kernel}'; choose one of: {', '.join(names)}")
+        self.kernel = names[kernel]
+        self.last_kernel: str | None = None
+
+    # ------------------------------------------------------------ probe ---
+    def probe(self, device: torch.device) -> BackendAvailability:
+        device = torch.device(device)
+
+        def no(reason: str) -> BackendAvailability:
+            return BackendAvailability(self.name, False, True, False, reason, device.type)
+
+        if device.type != "cuda":
+            return no(f"HIP backend requires a ROCm GPU device, got {device.type}")
+        if torch.version.hip is None:
+            return no("HIP backend requires a ROCm build of PyTorch")
+        if not torch.cuda.is_available():
+            return no("no ROCm GPU is visible")
+        ok, why = _native.available()
+        if not ok:
+            return no(why)
+        index = _index(device)
+        if index not in _device_state:
+            _device_state[index] = _native.device_ok(index)
+        ok, why = _device_state[index]
+        if not ok:
+            return no(why)
+        return BackendAvailability(self.name, True, True, False, f"fused HIP kernels on {why}", device.type)
+
+    # -------------------------------------------------------------- run ---
+    def describe(
+        self, query: torch.Tensor, batch: PackedBatch, sm_scale: float, num_selected: int = 0
+    ) -> _native.DecodeDesc:
+        nb, bt, kvh, _ = batch.packed_k.shape
+        if query.dtype not in _native.QUERY_DTYPES:
+            raise ValueError(f"unsupported query dtype {query.dtype}")
+        return _native.DecodeDesc(
+            query_heads=query.shape[0],
+            kv_heads=kvh,
+            head_dim=query.shape[1],
+            num_blocks=nb,
+            block_tokens=bt,
+            bits=batch.bits,
+            group_size=batch.group_size,
+            query_dtype=_native.QUERY_DTYPES[query.dtype],
+            num_selected=num_selected,
+            kernel=self.kernel,
+            sm_scale=float(sm_scale),
+        )
+
+    def kernel_for(self, query: torch.Tensor, batch: PackedBatch, sm_scale: float = 1.0) -> str:
+        """Name of the kernel ``run`` would launch for this shape ("general" or "mfma")."""
+        desc = self.describe(query, batch, sm_scale)
+        out = ctypes.c_int(0)
+        _native.check(_native.load().kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(out)), "decode_kernel")
+        return _native.KERNEL_NAMES[out.value]
+
+    def run(
+        self,
+        query: torch.Tensor,
+        batch: PackedBatch,
+        sm_scale: float,
+        block_table: torch.Tensor | Sequence[int] | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Fused decode; with ``block_table`` attend over those block ids of the batch, in order."""
+        batch.validate(query)
+        if query.device.type != "cuda":
+            raise ValueError(f"HIP backend requires ROCm GPU tensors, got {query.device.type}")
+        if batch.packed_k.dtype != torch.uint8 or batch.packed_v.dtype != torch.uint8:
+            raise ValueError("packed KV must be uint8")
+        if batch.scales_k.dtype != torch.float16 or batch.scales_v.dtype != torch.float16:
+            raise ValueError("scales must be float16")
+        if batch.valid_tokens.dtype != torch.int32:
+            raise ValueError("valid_tokens must be int32")
+        if batch.scales_k.shape[:3] != batch.packed_k.shape[:3] or batch.scales_k.shape[3] != (
+            query.shape[1] // batch.group_size
+        ):
+            raise ValueError("scale dimension mismatch")
+        lib = _native.load()
+        table = None
+        if block_table is not None:
+            table = self._table(block_table, batch.packed_k.shape[0], query.device)
+        desc = self.describe(query, batch, sm_scale, 0 if table is None else table.numel())
+        q = query.contiguous()
+        pk, pv = batch.packed_k.contiguous(), batch.packed_v.contiguous()
+        sk, sv = batch.scales_k.contiguous(), batch.scales_v.contiguous()
+        valid = batch.valid_tokens.contiguous()
+        need = ctypes.c_size_t(0)
+        _native.check(lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(need)), "workspace")
+        kern = ctypes.c_int(0)
+        _native.check(lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(kern)), "decode_kernel")
+        with torch.cuda.device(query.device):
+            out = torch.empty((query.shape[0], query.shape[1]), dtype=torch.float32, device=query.device)
+            lse = torch.empty((query.shape[0],), dtype=torch.float32, device=query.device)
+            work = torch.empty((max(int(need.value), 1),), dtype=torch.uint8, device=query.device)
+            stream = torch.cuda.current_stream(query.device)
+            rc = lib.kvssd_hip_fused_decode(
+                ctypes.byref(desc),
+                _ptr(q),
+                _ptr(pk),
+                _ptr(pv),
+                _ptr(sk),
+                _ptr(sv),
+                _ptr(valid),
+                _ptr(table),
+                _ptr(out),
+                _ptr(lse),
+                _ptr(work),
+                work.numel(),
+                _native.stream_handle(stream),
+            )
+        _native.check(rc, "kvssd_hip_fused_decode")
+        self.last_kernel = _native.KERNEL_NAMES[kern.value]
+        return out, lse
+
+    @staticmethod
+    def _table(block_table, num_blocks: int, device: torch.device) -> torch.Tensor:
+        if isinstance(block_table, torch.Tensor):
+            if block_table.device.type == "cuda":
+                # validated by the caller that built it on the device; the
+                # kernels also skip ids outside [0, num_blocks)
+                return block_table.to(torch.int32).contiguous()
+            ids = block_table.to(torch.int64).tolist()
+        else:
+            ids = [int(x) for x in block_table]
+        if not ids:
+            raise ValueError("at least one block is required")
+        if min(ids) < 0 or max(ids) >= num_blocks:
+            raise ValueError(f"block ids must lie in [0, {num_blocks})")
+        return torch.tensor(ids, dtype=torch.int32).pin_memory().to(device, non_blocking=True)
+
+    # ----------------------------------------------------------- merge ---
+    def merge_chunks(
+        self, acc_out: torch.Tensor, acc_lse: torch.Tensor, out: torch.Tensor, lse: torch.Tensor
+    ) -> None:
+        """In-place exact merge (acc_out, acc_lse) <- merge((acc_out, acc_lse), (out, lse))."""
+        for t in (acc_out, acc_lse, out, lse):
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.device.type != "cuda":
+                raise ValueError("merge operands must be contiguous fp32 GPU tensors")
+        rows, dim = acc_out.shape
+        if out.shape != acc_out.shape or acc_lse.shape != (rows,) or lse.shape != (rows,):
+            raise ValueError("merge operand shapes differ")
+        stream = torch.cuda.current_stream(acc_out.device)
+        rc = _native.load().kvssd_hip_merge_chunks(
+            rows, dim, _ptr(acc_out), _ptr(acc_lse), _ptr(out), _ptr(lse), _native.stream_handle(stream)
+        )
+        _native.check(rc, "kvssd_hip_merge_chunks")

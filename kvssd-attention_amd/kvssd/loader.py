@@ -1,0 +1,93 @@
+"""Bounded prefetcher of KV records (reference: src/kvssd/loader.py:22-137).
+
+Reads stay on the host (O_DIRECT/preadv through the storage backend) in a
+small thread pool; ``depth`` reusable slots bound the bytes in flight.  Each
+yielded block owns copies of its four payload tensors, so recycling a slot can
+never corrupt a block a consumer still holds.
+"""
+
+from __future__ import annotations
+
+from collections import deque
+from concurrent.futures import Future, ThreadPoolExecutor
+from dataclasses import dataclass
+from queue import Queue
+from typing import Iterator
+
+import torch
+
+from .format import BlockEntry, PackedKVBlock, decode_record
+from .quant import QuantizedTensor
+from .store import KVCacheStore
+
+
+@dataclass
+class _Slot:
+    raw: torch.Tensor
+    future: Future[PackedKVBlock] | None = None
+
+
+def _detach(block: PackedKVBlock) -> PackedKVBlock:
+    def own(q: QuantizedTensor) -> QuantizedTensor:
+        return QuantizedTensor(q.packed.clone(), q.scales.clone(), q.original_shape, q.bits, q.group_size)
+
+    return PackedKVBlock(block.layer, block.block, block.valid_tokens, own(block.key), own(block.value))
+
+
+class AsyncBlockLoader:
+    """Bounded pinned-memory prefetcher; slots provide backpressure by construction."""
+
+    def __init__(
+        self,
+        store: KVCacheStore,
+        depth: int = 2,
+        pinned: bool = True,
+        device: torch.device | None = None,
+    ):
+        if depth < 1:
+            raise ValueError("depth must be positive")
+        self.store = store
+        self.device = device
+        self.executor = ThreadPoolExecutor(max_workers=depth, thread_name_prefix="kvssd-io")
+        self.free: Queue[_Slot] = Queue()
+        use_pinned = pinned and torch.cuda.is_available()
+        for _ in range(depth):
+            raw = store.storage_backend.allocate_buffer(store.spec.record_bytes, pinned=use_pinned, device=device)
+            self.free.put(_Slot(raw))
+
+    def iter_blocks(self, layer: int, block_ids: list[int]) -> Iterator[PackedKVBlock]:
+        pending: deque[tuple[_Slot, BlockEntry]] = deque()
+        todo = iter(block_ids)
+
+        def work(entry: BlockEntry, raw: torch.Tensor) -> PackedKVBlock:
+            # read, verify the CRC and copy the payloads out, all on the I/O
+            # thread; zlib and preadv release the GIL
+            self.store.read_into(entry, raw)
+            return _detach(decode_record(raw, self.store.spec))
+
+        def submit(block_id: int) -> None:
+            slot = self.free.get()
+            entry = self.store.entry(layer, block_id)
+            slot.future = self.executor.submit(work, entry, slot.raw)
+            pending.append((slot, entry))
+
+        for _ in range(min(self.free.qsize(), len(block_ids))):
+            submit(next(todo))
+        while pending:
+            slot, entry = pending.popleft()
+            assert slot.future is not None
+            block = slot.future.result()
+            nxt = next(todo, None)
+            self.free.put(slot)
+            if nxt is not None:
+                submit(nxt)
+            yield block
+
+    def close(self) -> None:
+        self.executor.shutdown(wait=True, cancel_futures=False)
+
+    def __enter__(self) -> "AsyncBlockLoader":
+        return self
+
+    def __exit__(self, *_: object) -> None:
+        self.close()

@@ -1,0 +1,247 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Bars (from the path's contract):
+  * unpacked integer codes and block selection: bit-exact;
+  * dequantised values: exact (fp32);
+  * attention out / lse: max-abs 2e-3, rel 1e-2 (fp32 accumulate), and the
+    general kernel also at the reference's own GPU tolerance 2e-4
+    (tests/test_triton_backend.py:110).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from kvssd import _native
+from kvssd.backends import PackedBatch, resolve_attention_backend
+from kvssd.backends.hip import HipAttentionBackend
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2  # contract tolerance
+REF_TOL = 2e-4  # reference GPU-test tolerance
+
+
+def make_batch(seed, qh, kvh, d, nb, bt, bits, g, valid=None, value_scale=1.0, outliers=0.0):
+    rng = np.random.default_rng(seed)
+    k = (rng.standard_normal((nb * bt, kvh, d)) * value_scale).astype(np.float32)
+    v = (rng.standard_normal((nb * bt, kvh, d)) * value_scale).astype(np.float32)
+    if outliers:
+        k[rng.random(k.shape) < outliers] *= 8
+        v[rng.random(v.shape) < outliers] *= 8
+    q = rng.standard_normal((qh, d)).astype(np.float32)
+    pk, sk, _ = O.quantize_blocks(k, bits, g, bt)
+    pv, sv, _ = O.quantize_blocks(v, bits, g, bt)
+    if valid is None:
+        valid = rng.integers(1, bt + 1, nb)
+    return q, pk, pv, sk, sv, np.asarray(valid, np.int32)
+
+
+def to_device(dev, q, pk, pv, sk, sv, valid, bits, g, qdtype=torch.float32):
+    query = torch.from_numpy(q).to(qdtype).to(dev)
+    batch = PackedBatch(
+        torch.from_numpy(pk).to(dev),
+        torch.from_numpy(pv).to(dev),
+        torch.from_numpy(sk).to(dev),
+        torch.from_numpy(sv).to(dev),
+        torch.from_numpy(valid).to(dev),
+        bits,
+        g,
+    )
+    return query, batch
+
+
+def check(out, lse, ref_out, ref_lse, atol=ATOL, rtol=RTOL):
+    out, lse = out.cpu().numpy(), lse.cpu().numpy()
+    np.testing.assert_allclose(out, ref_out, atol=atol, rtol=rtol)
+    np.testing.assert_allclose(lse, ref_lse, atol=atol, rtol=rtol)
+
+
+def kernels_for(qh, kvh, d, g):
+    names = ["general"]
+    probe = HipAttentionBackend("auto")
+    q = torch.zeros(qh, d)
+    nb = torch.zeros(1, 16, kvh, d // 2, dtype=torch.uint8)
+    ns = torch.zeros(1, 16, kvh, d // g, dtype=torch.float16)
+    if probe.kernel_for(q, PackedBatch(nb, nb, ns, ns, torch.ones(1, dtype=torch.int32), 4, g)) == "mfma":
+        names.append("mfma")
+    return names
+
+
+# ------------------------------------------------------------------ codec ---
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("n_bytes", [1, 3, 256, 4096 + 7, 1 << 20])
+def test_unpack_codes_bit_exact(cuda_device, bits, n_bytes):
+    rng = np.random.default_rng(n_bytes)
+    packed = rng.integers(0, 256, n_bytes, dtype=np.uint8)
+    packed[: min(256, n_bytes)] = np.arange(min(256, n_bytes), dtype=np.uint8)  # every byte value
+    src = torch.from_numpy(packed).to(cuda_device)
+    dst = torch.full((n_bytes * 8 // bits,), 255, dtype=torch.uint8, device=cuda_device)
+    rc = _native.load().kvssd_hip_unpack_codes(src.data_ptr(), bits, n_bytes, dst.data_ptr(), None)
+    _native.check(rc, "unpack")
+    torch.cuda.synchronize()
+    assert np.array_equal(dst.cpu().numpy(), O.unpack_np(packed, bits))
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("g", [16, 32, 128])
+def test_dequantize_exact(cuda_device, bits, g):
+    rng = np.random.default_rng(g + bits)
+    x = (rng.standard_normal((300, 128)) * rng.choice([1e-4, 1.0, 100.0], (300, 1))).astype(np.float32)
+    codes, scales = O.quantize_c(x, bits, g)
+    packed = O.pack_np(codes, bits)
+    out = torch.empty((300, 128), dtype=torch.float32, device=cuda_device)
+    p = torch.from_numpy(packed).to(cuda_device)
+    s = torch.from_numpy(scales.view(np.uint16).copy()).to(cuda_device)
+    rc = _native.load().kvssd_hip_dequantize(p.data_ptr(), s.data_ptr(), 300, 128, bits, g, out.data_ptr(), None)
+    _native.check(rc, "dequantize")
+    assert np.array_equal(out.cpu().numpy(), O.dequantize_np(codes, scales, bits, g))
+
+
+# ---------------------------------------------------------------- decode ---
+
+MATRIX = [(1, 1, 32, 16), (4, 1, 64, 16), (4, 2, 128, 16), (4, 2, 128, 32), (32, 8, 128, 32), (64, 8, 128, 32)]
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize(("qh", "kvh", "d", "g"), MATRIX)
+def test_decode_matrix_fp32_query(cuda_device, bits, qh, kvh, d, g):
+    q, pk, pv, sk, sv, valid = make_batch(41, qh, kvh, d, 5, 32, bits, g)
+    scale = 1 / math.sqrt(d)
+    ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, g, scale)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, g)
+    for kernel in kernels_for(qh, kvh, d, g):
+        backend = HipAttentionBackend(kernel)
+        out, lse = backend.run(query, batch, scale)
+        assert backend.last_kernel == kernel
+        tol = REF_TOL if kernel == "general" else ATOL
+        check(out, lse, ref_out, ref_lse, atol=tol, rtol=REF_TOL if kernel == "general" else RTOL)
+
+
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("bits", [2, 4])
+def test_decode_query_dtypes(cuda_device, qdtype, bits):
+    q, pk, pv, sk, sv, valid = make_batch(7, 32, 8, 128, 4, 128, bits, 32)
+    q = torch.from_numpy(q).to(qdtype).double().float().numpy()  # the values the kernel sees
+    scale = 1 / math.sqrt(128)
+    ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, 32, scale)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, qdtype)
+    for kernel in kernels_for(32, 8, 128, 32):
+        out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
+        check(out, lse, ref_out, ref_lse)
+
+
+def test_decode_reference_test_shapes_block_tokens_8(cuda_device):
+    # tests/test_triton_backend.py:13-31: 2 blocks x 8 tokens, valid [8, 5], g=16
+    for bits in (2, 4):
+        for qh, kvh, d in [(1, 1, 32), (4, 1, 64), (4, 2, 128)]:
+            q, pk, pv, sk, sv, _ = make_batch(41, qh, kvh, d, 2, 8, bits, 16)
+            valid = np.array([8, 5], np.int32)
+            scale = 1 / math.sqrt(d)
+            ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, 16, scale)
+            query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 16)
+            out, lse = resolve_attention_backend("hip", cuda_device).run(query, batch, scale)
+            check(out, lse, ref_out, ref_lse, atol=REF_TOL, rtol=REF_TOL)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_decode_edge_cases(cuda_device, bits):
+    q, pk, pv, sk, sv, _ = make_batch(3, 32, 8, 128, 6, 64, bits, 32)
+    scale = 0.1
+    cases = {
+        "zero_blocks": np.array([64, 0, 17, 0, 1, 64], np.int32),
+        "oversize_and_negative": np.array([99, -4, 64, 3, 1000, 2], np.int32),
+        "single_token": np.array([0, 0, 0, 1, 0, 0], np.int32),
+    }
+    for name, valid in cases.items():
+        ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, 32, scale)
+        query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32)
+        for kernel in kernels_for(32, 8, 128, 32):
+            out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
+            check(out, lse, ref_out, ref_lse)
+    # no valid token at all: out = 0, lse = -inf (what the reference backend returns)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, np.zeros(6, np.int32), bits, 32)
+    for kernel in kernels_for(32, 8, 128, 32):
+        out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
+        assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
+
+
+def test_decode_padding_garbage_is_ignored(cuda_device):
+    q, pk, pv, sk, sv, valid = make_batch(4, 32, 8, 128, 3, 64, 4, 32, valid=[64, 10, 33])
+    ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.1)
+    rng = np.random.default_rng(0)
+    for b, n in enumerate(valid):
+        pk[b, n:] = rng.integers(0, 256, pk[b, n:].shape)
+        pv[b, n:] = rng.integers(0, 256, pv[b, n:].shape)
+        sk[b, n:] = np.float16(np.inf)
+        sv[b, n:] = np.float16(np.nan)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, 4, 32)
+    for kernel in kernels_for(32, 8, 128, 32):
+        out, lse = HipAttentionBackend(kernel).run(query, batch, 0.1)
+        check(out, lse, ref_out, ref_lse)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_block_table_selection(cuda_device, bits):
+    q, pk, pv, sk, sv, valid = make_batch(8, 64, 8, 128, 40, 128, bits, 32)
+    avail = list(range(40))
+    for sink, recent in [(1, 32), (2, 3), (0, 1), (5, 0)]:
+        ids = O.select_recent_sink(avail, sink, recent)
+        table = np.array(ids, np.int32)
+        ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, 32, 0.09, block_table=table)
+        query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32)
+        for kernel in kernels_for(64, 8, 128, 32):
+            out, lse = HipAttentionBackend(kernel).run(query, batch, 0.09, block_table=ids)
+            check(out, lse, ref_out, ref_lse)
+    with pytest.raises(ValueError, match="block ids"):
+        HipAttentionBackend().run(query, batch, 0.09, block_table=[0, 40])
+
+
+def test_config_cpu_runnable_4096_tokens(cuda_device):
+    # 1 layer, 4096 tokens, KVH 8, QH 32, D 128, BT 128, INT4 g32, fp16 query
+    gen = torch.Generator().manual_seed(7)
+    k = torch.randn(4096, 8, 128, generator=gen, dtype=torch.float16)
+    v = torch.randn(4096, 8, 128, generator=gen, dtype=torch.float16)
+    q = torch.randn(32, 128, generator=gen, dtype=torch.float16)
+    pk, sk, valid = O.quantize_blocks(k.float().numpy(), 4, 32, 128)
+    pv, sv, _ = O.quantize_blocks(v.float().numpy(), 4, 32, 128)
+    scale = 1 / math.sqrt(128)
+    ref_out, ref_lse = O.attention(q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, scale)
+    query, batch = to_device(cuda_device, q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, torch.float16)
+    for kernel in kernels_for(32, 8, 128, 32):
+        out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
+        check(out, lse, ref_out, ref_lse)
+
+
+def test_merge_chunks_kernel(cuda_device):
+    q, pk, pv, sk, sv, valid = make_batch(12, 32, 8, 128, 6, 32, 4, 32)
+    halves = [slice(0, 2), slice(2, 6)]
+    parts = [O.attention(q, pk[s], pv[s], sk[s], sv[s], valid[s], 4, 32, 0.1) for s in halves]
+    full_out, full_lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.1)
+    acc_o = torch.from_numpy(parts[0][0]).to(cuda_device)
+    acc_l = torch.from_numpy(parts[0][1]).to(cuda_device)
+    HipAttentionBackend().merge_chunks(
+        acc_o, acc_l, torch.from_numpy(parts[1][0]).to(cuda_device), torch.from_numpy(parts[1][1]).to(cuda_device)
+    )
+    check(acc_o, acc_l, full_out, full_lse, atol=1e-5, rtol=1e-5)
+    empty_o = torch.full_like(acc_o, float("nan"))
+    empty_l = torch.full_like(acc_l, float("-inf"))
+    before = acc_o.clone()
+    HipAttentionBackend().merge_chunks(acc_o, acc_l, empty_o, empty_l)
+    torch.testing.assert_close(acc_o, before)
+
+
+def test_library_shares_torch_hip_runtime(cuda_device):
+    HipAttentionBackend().probe(cuda_device)
+    maps = open("/proc/self/maps").read()
+    paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(paths) == 1, paths
+    assert any("libkvssd_hip.so" in line for line in maps.splitlines())

@@ -1,0 +1,127 @@
+"""GPU pipeline parity (streamed SSD -> pinned staging -> HIP kernels, and
+HBM-resident layers) and full-size properties of the 128K-token workload."""
+
+from __future__ import annotations
+
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from kvssd import KVCacheStore, KVSSDPipeline
+from kvssd.backends import PackedBatch
+from kvssd.backends.hip import HipAttentionBackend
+from kvssd.format import CacheSpec
+from kvssd.selectors import AllBlocks, RecentSinkBlocks
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-3, 1e-2
+
+
+def build_store(path: Path, tokens: int, bits: int, kvh: int = 8, d: int = 128, bt: int = 128, g: int = 32):
+    gen = torch.Generator().manual_seed(tokens + bits)
+    keys = torch.randn(1, tokens, kvh, d, generator=gen, dtype=torch.float16)
+    values = torch.randn(1, tokens, kvh, d, generator=gen, dtype=torch.float16)
+    store = KVCacheStore.create(path, keys, values, CacheSpec(1, kvh, d, bt, bits, g))
+    pk, sk, valid = O.quantize_blocks(keys[0].float().numpy(), bits, g, bt)
+    pv, sv, _ = O.quantize_blocks(values[0].float().numpy(), bits, g, bt)
+    return store, (pk, pv, sk, sv, valid)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("stage_blocks", [1, 3, 8])
+def test_streamed_pipeline_matches_oracle(cuda_device, tmp_path: Path, bits: int, stage_blocks: int):
+    store, (pk, pv, sk, sv, valid) = build_store(tmp_path, 2500, bits)  # 20 blocks, last one partial
+    query = torch.randn(32, 128, generator=torch.Generator().manual_seed(1), dtype=torch.float16)
+    scale = 1 / math.sqrt(128)
+    with KVSSDPipeline(store, device=cuda_device, stage_blocks=stage_blocks, attention_backend="hip") as pipe:
+        assert pipe.attention_backend.name == "hip"
+        for selector in (AllBlocks(), RecentSinkBlocks(1, 4), RecentSinkBlocks(2, 0)):
+            out = pipe.decode(query, 0, selector)
+            assert out.dtype == torch.float16 and out.device.type == "cuda"
+            ids = np.array(selector.select(list(range(20))), np.int32)
+            ref, _ = O.attention(query.float().numpy(), pk, pv, sk, sv, valid, bits, 32, scale, block_table=ids)
+            np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+
+
+def test_resident_pipeline_matches_streamed(cuda_device, tmp_path: Path):
+    store, (pk, pv, sk, sv, valid) = build_store(tmp_path, 4096, 4)
+    query = torch.randn(32, 128, generator=torch.Generator().manual_seed(2), dtype=torch.float16)
+    with KVSSDPipeline(store, device=cuda_device, stage_blocks=4, attention_backend="hip") as pipe:
+        streamed = pipe.decode(query, 0, RecentSinkBlocks(1, 8))
+        pipe.load_resident([0])
+        resident = pipe.decode(query, 0, RecentSinkBlocks(1, 8))
+        full = pipe.decode(query, 0)
+    ids = np.array([0] + list(range(24, 32)), np.int32)
+    ref, _ = O.attention(query.float().numpy(), pk, pv, sk, sv, valid, 4, 32, 1 / math.sqrt(128), block_table=ids)
+    np.testing.assert_allclose(resident.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(streamed.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    ref_full, _ = O.attention(query.float().numpy(), pk, pv, sk, sv, valid, 4, 32, 1 / math.sqrt(128))
+    np.testing.assert_allclose(full.float().cpu().numpy(), ref_full, atol=ATOL, rtol=RTOL)
+
+
+def test_require_cuda_kernel_runs_hip(cuda_device, tmp_path: Path):
+    store, _ = build_store(tmp_path, 300, 4)
+    with KVSSDPipeline(store, device=cuda_device, require_cuda_kernel=True) as pipe:
+        assert pipe.attention_backend.name == "hip"
+        out = pipe.decode(torch.randn(32, 128, dtype=torch.float16), 0)
+        assert torch.isfinite(out).all()
+
+
+def synth_packed(tokens: int, bits: int, seed: int, value_scale: float = 1.0, outliers: float = 0.0, qh: int = 32):
+    """Quantised synthetic KV [T, 8, 128] in PackedBatch layout (numpy) + fp16 query."""
+    gen = torch.Generator().manual_seed(seed)
+    k = torch.randn(tokens, 8, 128, generator=gen, dtype=torch.float16)
+    v = torch.randn(tokens, 8, 128, generator=gen, dtype=torch.float16)
+    q = torch.randn(qh, 128, generator=gen, dtype=torch.float16)
+    k, v = (k.float() * value_scale), (v.float() * value_scale)
+    if outliers:
+        m = torch.rand(k.shape, generator=gen) < outliers
+        k[m] *= 8
+        v[torch.rand(v.shape, generator=gen) < outliers] *= 8
+    pk, sk, valid = O.quantize_blocks(k.half().float().numpy(), bits, 32, 128)
+    pv, sv, _ = O.quantize_blocks(v.half().float().numpy(), bits, 32, 128)
+    return q, (pk, pv, sk, sv, valid)
+
+
+@pytest.mark.parametrize(("bits", "value_scale", "outliers"), [(4, 0.5, 0.0), (2, 1.0, 0.05)])
+def test_full_size_128k_tokens(cuda_device, bits, value_scale, outliers):
+    # the 131072-token INT4 (x0.5 values) and INT2 (5% x8 outliers) workloads:
+    # parity with the oracle at full size, plus the size-independent split property
+    q, (pk, pv, sk, sv, valid) = synth_packed(131072, bits, 7, value_scale, outliers)
+    scale = 1 / math.sqrt(128)
+    ref_out, ref_lse = O.attention(q.float().numpy(), pk, pv, sk, sv, valid, bits, 32, scale, threads=16)
+    dev = cuda_device
+    query = q.to(dev)
+    batch = PackedBatch(*(torch.from_numpy(a).to(dev) for a in (pk, pv, sk, sv, valid)), bits, 32)
+    for kernel in ["general", "mfma"]:
+        backend = HipAttentionBackend(kernel if kernel == "general" else "auto")
+        out, lse = backend.run(query, batch, scale)
+        np.testing.assert_allclose(out.cpu().numpy(), ref_out, atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=ATOL, rtol=RTOL)
+        # any split of the block range merges back to the one-call result
+        a_out, a_lse = backend.run(query, PackedBatch(*(x[:333] for x in (batch.packed_k, batch.packed_v, batch.scales_k, batch.scales_v, batch.valid_tokens)), bits, 32), scale)
+        b_out, b_lse = backend.run(query, PackedBatch(*(x[333:] for x in (batch.packed_k, batch.packed_v, batch.scales_k, batch.scales_v, batch.valid_tokens)), bits, 32), scale)
+        backend.merge_chunks(a_out, a_lse, b_out, b_lse)
+        torch.testing.assert_close(a_out, out, atol=1e-4, rtol=1e-3)
+        torch.testing.assert_close(a_lse, lse, atol=1e-4, rtol=1e-4)
+
+
+def test_sparse_selection_262k_tokens(cuda_device):
+    # 262144 tokens, GQA 8, RecentSinkBlocks(1, 32) -> 33 non-contiguous blocks
+    q, (pk, pv, sk, sv, valid) = synth_packed(262144, 4, 11, qh=64)
+    ids = RecentSinkBlocks(1, 32).select(list(range(2048)))
+    assert ids == [0] + list(range(2016, 2048))
+    table = np.array(ids, np.int32)
+    scale = 1 / math.sqrt(128)
+    ref_out, ref_lse = O.attention(q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, scale, block_table=table)
+    dev = cuda_device
+    batch = PackedBatch(*(torch.from_numpy(a).to(dev) for a in (pk, pv, sk, sv, valid)), 4, 32)
+    for kernel in ["general", "auto"]:
+        out, lse = HipAttentionBackend(kernel).run(q.to(dev), batch, scale, block_table=ids)
+        np.testing.assert_allclose(out.cpu().numpy(), ref_out, atol=ATOL, rtol=RTOL)
+        np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=ATOL, rtol=RTOL)
