@@ -69,15 +69,6 @@ int choose_kernel(const kvssd_decode_desc& d, int* kernel) {
   return 0;
 }
 
-int plan_splits(const kvssd_decode_desc& d, int units, int kernel, int* splits) {
-  if (kernel == KVSSD_KERNEL_MFMA) {
-    *splits = plan_mfma(d, units).splits;
-  } else {
-    *splits = plan_general(d, units).splits;
-  }
-  return 0;
-}
-
 int units_of(const kvssd_decode_desc* d, const int32_t* table, int* units) {
   if (table != nullptr) {
     if (d->num_selected <= 0) return arg_error("at least one block is required");
@@ -92,7 +83,7 @@ int prepare(const kvssd_decode_desc* desc, const int32_t* table, void* workspace
   if (int rc = validate(desc, units)) return rc;
   if (int rc = units_of(desc, table, units)) return rc;
   if (int rc = choose_kernel(*desc, kernel)) return rc;
-  plan_splits(*desc, *units, *kernel, splits);
+  *splits = plan_splits(*desc, *units).splits;
   const size_t need = split_partial_bytes(*splits, desc->query_heads, desc->head_dim);
   if (workspace == nullptr || workspace_bytes < need)
     return arg_error("workspace too small: need " + std::to_string(need) + " bytes");
@@ -159,9 +150,7 @@ __attribute__((visibility("default"))) int kvssd_hip_decode_workspace_bytes(cons
   if (desc->num_selected > 0) units = desc->num_selected;
   int kernel = 0;
   if (int rc = choose_kernel(*desc, &kernel)) return rc;
-  int splits = 0;
-  plan_splits(*desc, units, kernel, &splits);
-  *bytes = split_partial_bytes(splits, desc->query_heads, desc->head_dim);
+  *bytes = split_partial_bytes(plan_splits(*desc, units).splits, desc->query_heads, desc->head_dim);
   return 0;
 }
 
@@ -185,8 +174,13 @@ __attribute__((visibility("default"))) int kvssd_hip_decode_partials(
   a.units = units;
   a.stream = static_cast<hipStream_t>(stream);
   SplitPartials parts = carve_partials(workspace, splits, desc->query_heads, desc->head_dim);
-  if (kernel == KVSSD_KERNEL_MFMA) return launch_mfma(a, plan_mfma(*desc, units), parts);
-  return launch_general(a, plan_general(*desc, units), parts);
+  const SplitPlan plan = plan_splits(*desc, units);
+  if (kernel == KVSSD_KERNEL_MFMA) {
+    if (mfma_aligned(a)) return launch_mfma(a, plan, parts);
+    if (desc->kernel == KVSSD_KERNEL_MFMA)
+      return arg_error("matrix-core kernel needs 16-byte aligned packed arrays (8-byte for INT2) and 8-byte aligned scales");
+  }
+  return launch_general(a, plan, parts);
 }
 
 __attribute__((visibility("default"))) int kvssd_hip_decode_merge(const kvssd_decode_desc* desc,

@@ -20,25 +20,21 @@ struct DecodeArgs {
   hipStream_t stream;
 };
 
-// ---- general kernel: any head_dim <= 256, group size, GQA ratio, block size
-struct GeneralPlan {
-  int splits;           // token-axis splits (grid.x)
-  int blocks_per_split; // consecutive units per split
-  int heads_per_chunk;  // query heads per workgroup (<= 8)
-  int head_chunks;      // workgroups per kv head along the query-head axis
+// ---- split-K plan, shared by every kernel so the workspace size and the
+// merge depend only on the shape, never on which kernel ran
+struct SplitPlan {
+  int splits;            // partitions of the attended blocks
+  int blocks_per_split;  // consecutive attended blocks per partition
 };
-GeneralPlan plan_general(const kvssd_decode_desc& d, int units);
-int launch_general(const DecodeArgs& a, const GeneralPlan& plan, SplitPartials parts);
+SplitPlan plan_splits(const kvssd_decode_desc& d, int units);
+
+// ---- general kernel: any head_dim <= 256, group size, GQA ratio, block size
+int launch_general(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts);
 
 // ---- matrix-core kernel: head_dim 128, group_size 32, bits 2/4
-struct MfmaPlan {
-  int splits;           // waves per kv head along the token axis
-  int blocks_per_split; // units per wave
-  int head_quads;       // groups of 4 query heads per kv head
-};
 bool mfma_supported(const kvssd_decode_desc& d, std::string* why);
-MfmaPlan plan_mfma(const kvssd_decode_desc& d, int units);
-int launch_mfma(const DecodeArgs& a, const MfmaPlan& plan, SplitPartials parts);
+bool mfma_aligned(const DecodeArgs& a);
+int launch_mfma(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts);
 
 // ---- split-K phase 2: merge the partials of every split into (out, lse)
 int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, float* out, float* lse,

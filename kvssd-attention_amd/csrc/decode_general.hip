@@ -183,23 +183,21 @@ int launch_typed(const GeneralParams& prm, dim3 grid, int bits, hipStream_t s) {
 
 }  // namespace
 
-GeneralPlan plan_general(const kvssd_decode_desc& d, int units) {
-  GeneralPlan plan{};
-  const int gq = d.query_heads / d.kv_heads;
-  plan.heads_per_chunk = gq < kMaxHeads ? gq : kMaxHeads;
-  plan.head_chunks = (gq + plan.heads_per_chunk - 1) / plan.heads_per_chunk;
-  // about 1024 workgroups in total (4 per CU on a 256-CU part)
-  const long others = static_cast<long>(d.kv_heads) * plan.head_chunks;
-  long target = 1024 / (others > 0 ? others : 1);
-  if (target < 1) target = 1;
-  plan.blocks_per_split = static_cast<int>((units + target - 1) / target);
-  if (plan.blocks_per_split < 1) plan.blocks_per_split = 1;
+SplitPlan plan_splits(const kvssd_decode_desc& d, int units) {
+  // about 2048 (kv head, split) work items: 8 waves per CU on a 256-CU part
+  // for the matrix-core kernel, 2048+ four-wave workgroups for the general one
+  long per = (static_cast<long>(units) * d.kv_heads + 2047) / 2048;
+  SplitPlan plan{};
+  plan.blocks_per_split = static_cast<int>(per < 1 ? 1 : per);
   plan.splits = (units + plan.blocks_per_split - 1) / plan.blocks_per_split;
   return plan;
 }
 
-int launch_general(const DecodeArgs& a, const GeneralPlan& plan, SplitPartials parts) {
+int launch_general(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts) {
   const kvssd_decode_desc& d = a.desc;
+  const int gq = d.query_heads / d.kv_heads;
+  const int heads_per_chunk = gq < kMaxHeads ? gq : kMaxHeads;
+  const int head_chunks = (gq + heads_per_chunk - 1) / heads_per_chunk;
   GeneralParams prm{};
   prm.query = a.query;
   prm.pk = a.packed_k;
@@ -220,10 +218,10 @@ int launch_general(const DecodeArgs& a, const GeneralPlan& plan, SplitPartials p
   prm.packed_dim = d.head_dim * d.bits / 8;
   prm.units = a.units;
   prm.blocks_per_split = plan.blocks_per_split;
-  prm.heads_per_chunk = plan.heads_per_chunk;
-  prm.head_chunks = plan.head_chunks;
+  prm.heads_per_chunk = heads_per_chunk;
+  prm.head_chunks = head_chunks;
   prm.scale_log2 = static_cast<float>(d.sm_scale) * kLog2e;
-  dim3 grid(plan.splits, d.kv_heads * plan.head_chunks);
+  dim3 grid(plan.splits, d.kv_heads * head_chunks);
   switch (d.query_dtype) {
     case KVSSD_DTYPE_F16:
       return launch_typed<_Float16>(prm, grid, d.bits, a.stream);

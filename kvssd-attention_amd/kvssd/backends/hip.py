@@ -152,8 +152,16 @@ class HipAttentionBackend:
                 _native.stream_handle(stream),
             )
         _native.check(rc, "kvssd_hip_fused_decode")
-        self.last_kernel = _native.KERNEL_NAMES[kern.value]
+        name = _native.KERNEL_NAMES[kern.value]
+        if name == "mfma" and not self._mfma_aligned(batch.bits, pk, pv, sk, sv):
+            name = "general"  # the library's AUTO choice for buffers it cannot load 16 B at a time
+        self.last_kernel = name
         return out, lse
+
+    @staticmethod
+    def _mfma_aligned(bits: int, pk, pv, sk, sv) -> bool:
+        need = 16 if bits == 4 else 8
+        return all(t.data_ptr() % need == 0 for t in (pk, pv)) and all(t.data_ptr() % 8 == 0 for t in (sk, sv))
 
     @staticmethod
     def _table(block_table, num_blocks: int, device: torch.device) -> torch.Tensor:

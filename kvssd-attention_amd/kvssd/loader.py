@@ -4,6 +4,11 @@ Reads stay on the host (O_DIRECT/preadv through the storage backend) in a
 small thread pool; ``depth`` reusable slots bound the bytes in flight.  Each
 yielded block owns copies of its four payload tensors, so recycling a slot can
 never corrupt a block a consumer still holds.
+
+The slots are pageable host memory even when ``pinned=True`` is passed: on
+ROCm, page-locked memory from the HIP runtime is not a valid O_DIRECT target
+(``preadv`` fails with EFAULT), and the slots are only bounce buffers anyway;
+the pipeline's page-locked staging ring is what crosses PCIe.
 """
 
 from __future__ import annotations
@@ -50,9 +55,9 @@ class AsyncBlockLoader:
         self.device = device
         self.executor = ThreadPoolExecutor(max_workers=depth, thread_name_prefix="kvssd-io")
         self.free: Queue[_Slot] = Queue()
-        use_pinned = pinned and torch.cuda.is_available()
+        del pinned  # see the module docstring: slots stay pageable
         for _ in range(depth):
-            raw = store.storage_backend.allocate_buffer(store.spec.record_bytes, pinned=use_pinned, device=device)
+            raw = store.storage_backend.allocate_buffer(store.spec.record_bytes, pinned=False, device=device)
             self.free.put(_Slot(raw))
 
     def iter_blocks(self, layer: int, block_ids: list[int]) -> Iterator[PackedKVBlock]:

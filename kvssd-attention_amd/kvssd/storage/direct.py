@@ -55,8 +55,10 @@ class DirectIOStorageBackend:
         pinned: bool = False,
         device: torch.device | None = None,
     ) -> torch.Tensor:
-        del device
-        return aligned_host_buffer(size, pinned=pinned)
+        # ROCm page-locked memory is not a valid O_DIRECT target (preadv fails
+        # with EFAULT), so direct-read buffers are always pageable.
+        del device, pinned
+        return aligned_host_buffer(size, pinned=False)
 
     def read_into(self, entry: BlockEntry, destination: torch.Tensor) -> None:
         if destination.device.type != "cpu" or destination.dtype != torch.uint8:

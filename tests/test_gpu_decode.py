@@ -63,13 +63,10 @@ def check(out, lse, ref_out, ref_lse, atol=ATOL, rtol=RTOL):
     np.testing.assert_allclose(lse, ref_lse, atol=atol, rtol=rtol)
 
 
-def kernels_for(qh, kvh, d, g):
+def kernels_for(query, batch):
+    """Every kernel that supports this shape ("general" always, "mfma" when it applies)."""
     names = ["general"]
-    probe = HipAttentionBackend("auto")
-    q = torch.zeros(qh, d)
-    nb = torch.zeros(1, 16, kvh, d // 2, dtype=torch.uint8)
-    ns = torch.zeros(1, 16, kvh, d // g, dtype=torch.float16)
-    if probe.kernel_for(q, PackedBatch(nb, nb, ns, ns, torch.ones(1, dtype=torch.int32), 4, g)) == "mfma":
+    if HipAttentionBackend("auto").kernel_for(query, batch) == "mfma":
         names.append("mfma")
     return names
 
@@ -108,17 +105,29 @@ def test_dequantize_exact(cuda_device, bits, g):
 
 # ---------------------------------------------------------------- decode ---
 
-MATRIX = [(1, 1, 32, 16), (4, 1, 64, 16), (4, 2, 128, 16), (4, 2, 128, 32), (32, 8, 128, 32), (64, 8, 128, 32)]
+MATRIX = [
+    (1, 1, 32, 16, 32),
+    (4, 1, 64, 16, 32),
+    (4, 2, 128, 16, 32),
+    (4, 2, 128, 32, 32),
+    (1, 1, 128, 32, 128),
+    (2, 1, 128, 32, 128),
+    (4, 1, 128, 32, 128),
+    (12, 2, 128, 32, 128),
+    (32, 8, 128, 32, 128),
+    (64, 8, 128, 32, 128),
+    (32, 8, 128, 32, 256),
+]
 
 
 @pytest.mark.parametrize("bits", [2, 4])
-@pytest.mark.parametrize(("qh", "kvh", "d", "g"), MATRIX)
-def test_decode_matrix_fp32_query(cuda_device, bits, qh, kvh, d, g):
-    q, pk, pv, sk, sv, valid = make_batch(41, qh, kvh, d, 5, 32, bits, g)
+@pytest.mark.parametrize(("qh", "kvh", "d", "g", "bt"), MATRIX)
+def test_decode_matrix_fp32_query(cuda_device, bits, qh, kvh, d, g, bt):
+    q, pk, pv, sk, sv, valid = make_batch(41, qh, kvh, d, 5, bt, bits, g)
     scale = 1 / math.sqrt(d)
     ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, g, scale)
     query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, g)
-    for kernel in kernels_for(qh, kvh, d, g):
+    for kernel in kernels_for(query, batch):
         backend = HipAttentionBackend(kernel)
         out, lse = backend.run(query, batch, scale)
         assert backend.last_kernel == kernel
@@ -134,7 +143,8 @@ def test_decode_query_dtypes(cuda_device, qdtype, bits):
     scale = 1 / math.sqrt(128)
     ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, 32, scale)
     query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, qdtype)
-    for kernel in kernels_for(32, 8, 128, 32):
+    assert "mfma" in kernels_for(query, batch)
+    for kernel in kernels_for(query, batch):
         out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
         check(out, lse, ref_out, ref_lse)
 
@@ -154,28 +164,29 @@ def test_decode_reference_test_shapes_block_tokens_8(cuda_device):
 
 @pytest.mark.parametrize("bits", [2, 4])
 def test_decode_edge_cases(cuda_device, bits):
-    q, pk, pv, sk, sv, _ = make_batch(3, 32, 8, 128, 6, 64, bits, 32)
+    q, pk, pv, sk, sv, _ = make_batch(3, 32, 8, 128, 6, 256, bits, 32)
     scale = 0.1
     cases = {
-        "zero_blocks": np.array([64, 0, 17, 0, 1, 64], np.int32),
-        "oversize_and_negative": np.array([99, -4, 64, 3, 1000, 2], np.int32),
+        "zero_blocks": np.array([256, 0, 17, 0, 1, 129], np.int32),
+        "oversize_and_negative": np.array([999, -4, 256, 3, 1000, 128], np.int32),
         "single_token": np.array([0, 0, 0, 1, 0, 0], np.int32),
+        "sub_block_edges": np.array([127, 128, 129, 255, 16, 15], np.int32),
     }
     for name, valid in cases.items():
         ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, 32, scale)
         query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32)
-        for kernel in kernels_for(32, 8, 128, 32):
+        for kernel in kernels_for(query, batch):
             out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
             check(out, lse, ref_out, ref_lse)
     # no valid token at all: out = 0, lse = -inf (what the reference backend returns)
     query, batch = to_device(cuda_device, q, pk, pv, sk, sv, np.zeros(6, np.int32), bits, 32)
-    for kernel in kernels_for(32, 8, 128, 32):
+    for kernel in kernels_for(query, batch):
         out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
         assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
 
 
 def test_decode_padding_garbage_is_ignored(cuda_device):
-    q, pk, pv, sk, sv, valid = make_batch(4, 32, 8, 128, 3, 64, 4, 32, valid=[64, 10, 33])
+    q, pk, pv, sk, sv, valid = make_batch(4, 32, 8, 128, 3, 128, 4, 32, valid=[128, 10, 33])
     ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.1)
     rng = np.random.default_rng(0)
     for b, n in enumerate(valid):
@@ -184,7 +195,7 @@ def test_decode_padding_garbage_is_ignored(cuda_device):
         sk[b, n:] = np.float16(np.inf)
         sv[b, n:] = np.float16(np.nan)
     query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, 4, 32)
-    for kernel in kernels_for(32, 8, 128, 32):
+    for kernel in kernels_for(query, batch):
         out, lse = HipAttentionBackend(kernel).run(query, batch, 0.1)
         check(out, lse, ref_out, ref_lse)
 
@@ -198,7 +209,7 @@ def test_block_table_selection(cuda_device, bits):
         table = np.array(ids, np.int32)
         ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, bits, 32, 0.09, block_table=table)
         query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32)
-        for kernel in kernels_for(64, 8, 128, 32):
+        for kernel in kernels_for(query, batch):
             out, lse = HipAttentionBackend(kernel).run(query, batch, 0.09, block_table=ids)
             check(out, lse, ref_out, ref_lse)
     with pytest.raises(ValueError, match="block ids"):
@@ -216,7 +227,8 @@ def test_config_cpu_runnable_4096_tokens(cuda_device):
     scale = 1 / math.sqrt(128)
     ref_out, ref_lse = O.attention(q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, scale)
     query, batch = to_device(cuda_device, q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, torch.float16)
-    for kernel in kernels_for(32, 8, 128, 32):
+    assert kernels_for(query, batch) == ["general", "mfma"]
+    for kernel in kernels_for(query, batch):
         out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
         check(out, lse, ref_out, ref_lse)
 
@@ -245,3 +257,19 @@ def test_library_shares_torch_hip_runtime(cuda_device):
     paths = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
     assert len(paths) == 1, paths
     assert any("libkvssd_hip.so" in line for line in maps.splitlines())
+
+
+def test_misaligned_buffers_use_general_kernel(cuda_device):
+    q, pk, pv, sk, sv, valid = make_batch(5, 32, 8, 128, 2, 128, 4, 32)
+    ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.1)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, 4, 32)
+    raw = torch.empty(batch.packed_k.numel() + 8, dtype=torch.uint8, device=cuda_device)
+    shifted = raw[8:].view(batch.packed_k.shape)
+    shifted.copy_(batch.packed_k)
+    moved = PackedBatch(shifted, batch.packed_v, batch.scales_k, batch.scales_v, batch.valid_tokens, 4, 32)
+    auto = HipAttentionBackend("auto")
+    out, lse = auto.run(query, moved, 0.1)
+    assert auto.last_kernel == "general"
+    check(out, lse, ref_out, ref_lse)
+    with pytest.raises(ValueError, match="aligned"):
+        HipAttentionBackend("mfma").run(query, moved, 0.1)
