@@ -3,7 +3,7 @@
 // unpack_codes runs the same magic-number unpack the matrix-core kernel feeds
 // its MFMA operands with (common.hpp: unpack_int4_f16 / unpack_int2_f16), then
 // reads each fp16 lane back through a hardware fp16 -> fp32 conversion:
-//   code = 2^bits * (value - 1)   (value = 1 + code / 2^bits)
+//   code = F * (value - 1)   (value = 1 + code / F, F = 64 for INT4, 4 for INT2)
 // so any mistake in which code lands in which fp16 lane, or in the exponent
 // and mantissa placement, changes the output.  Twin of unpack_codes
 // (src/kvssd/quant.py:66-72).
@@ -38,8 +38,8 @@ __global__ void unpack_codes_kernel(const uint8_t* __restrict__ packed, int bits
     uint8_t c[8];
     // f[j] = (n_j, n_{j+4})
     for (int j = 0; j < 4; ++j) {
-      c[j] = code_from_f16(f[j], 0, 16.0f);
-      c[j + 4] = code_from_f16(f[j], 1, 16.0f);
+      c[j] = code_from_f16(f[j], 0, kUnpackScale<4>);
+      c[j + 4] = code_from_f16(f[j], 1, kUnpackScale<4>);
     }
     for (int i = 0; i < 2 * avail; ++i) codes[first * 2 + i] = c[i];
   } else {
@@ -48,8 +48,8 @@ __global__ void unpack_codes_kernel(const uint8_t* __restrict__ packed, int bits
     uint8_t c[16];
     // f[j] = (c_j, c_{j+8})
     for (int j = 0; j < 8; ++j) {
-      c[j] = code_from_f16(f[j], 0, 4.0f);
-      c[j + 8] = code_from_f16(f[j], 1, 4.0f);
+      c[j] = code_from_f16(f[j], 0, kUnpackScale<2>);
+      c[j + 8] = code_from_f16(f[j], 1, kUnpackScale<2>);
     }
     for (int i = 0; i < 4 * avail; ++i) codes[first * 4 + i] = c[i];
   }

@@ -96,10 +96,11 @@ __device__ __forceinline__ float wave_sum(float v) {
 //
 // A code c sits in the mantissa of an fp16 whose exponent field is that of
 // 1.0 (0x3C00):
-//   INT4: bits 6..9  -> value 1 + c/16, so c - 8 = 16 * (value - 1.5)
+//   INT4: bits 4..7  -> value 1 + c/64, so c - 8 = 64 * (value - 1.125)
 //   INT2: bits 8..9  -> value 1 + c/4,  so c - 2 =  4 * (value - 1.5)
-// i.e. (c - mid) = 2^bits * (value - 1.5) for both widths.  Each output word
-// holds two fp16 lanes (lo, hi).  One AND-OR plus at most one shift per word.
+// i.e. (c - mid) = F * (value - (1 + mid/F)) with F = kUnpackScale<bits>.
+// Each output word holds two fp16 lanes (lo, hi): one AND-OR per word plus at
+// most one shift (INT4: 3 shifts per 4 words' worth of 8 nibbles).
 //
 // INT4, x holds nibbles n0..n7 (n_i = bits 4i..4i+3, i.e. dims d0..d7 of a
 // packed row, low bits first):
@@ -107,25 +108,63 @@ __device__ __forceinline__ float wave_sum(float v) {
 // INT2, x holds codes c0..c15 (bits 2i..2i+1):
 //   w_j = (c_j, c_{j+8}) for j = 0..7.
 constexpr uint32_t kF16One2 = 0x3C003C00u;
+constexpr uint32_t kMaskInt4 = 0x00F000F0u;
+constexpr uint32_t kMaskInt2 = 0x03000300u;
+template <int BITS>
+constexpr float kUnpackScale = BITS == 4 ? 64.0f : 4.0f;     // F
+template <int BITS>
+constexpr float kUnpackOffset = BITS == 4 ? 1.125f : 1.5f;  // 1 + mid/F
+
+// (x & m) | c in one v_and_or_b32.  The backend splits this pattern into an
+// AND and an OR with literal operands (gfx9 allows one scalar/literal operand
+// per VALU instruction), so it is spelled out: m travels in a VGPR, c in an
+// SGPR.  Pure function (no side effects), so the compiler may still schedule,
+// hoist and CSE it.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "s"(c));
+  return r;
+}
 
 __device__ __forceinline__ void unpack_int4_f16(uint32_t x, uint32_t w[4]) {
-  constexpr uint32_t m = 0x03C003C0u;
-  w[0] = ((x << 6) & m) | kF16One2;
-  w[1] = ((x << 2) & m) | kF16One2;
-  w[2] = ((x >> 2) & m) | kF16One2;
-  w[3] = ((x >> 6) & m) | kF16One2;
+  const uint32_t m = kMaskInt4;
+  w[0] = and_or(x << 4, m, kF16One2);
+  w[1] = and_or(x, m, kF16One2);
+  w[2] = and_or(x >> 4, m, kF16One2);
+  w[3] = and_or(x >> 8, m, kF16One2);
 }
 
 __device__ __forceinline__ void unpack_int2_f16(uint32_t x, uint32_t w[8]) {
-  constexpr uint32_t m = 0x03000300u;
-  w[0] = ((x << 8) & m) | kF16One2;
-  w[1] = ((x << 6) & m) | kF16One2;
-  w[2] = ((x << 4) & m) | kF16One2;
-  w[3] = ((x << 2) & m) | kF16One2;
-  w[4] = (x & m) | kF16One2;
-  w[5] = ((x >> 2) & m) | kF16One2;
-  w[6] = ((x >> 4) & m) | kF16One2;
-  w[7] = ((x >> 6) & m) | kF16One2;
+  const uint32_t m = kMaskInt2;
+  w[0] = and_or(x << 8, m, kF16One2);
+  w[1] = and_or(x << 6, m, kF16One2);
+  w[2] = and_or(x << 4, m, kF16One2);
+  w[3] = and_or(x << 2, m, kF16One2);
+  w[4] = and_or(x, m, kF16One2);
+  w[5] = and_or(x >> 2, m, kF16One2);
+  w[6] = and_or(x >> 4, m, kF16One2);
+  w[7] = and_or(x >> 6, m, kF16One2);
+}
+
+// --- DPP row (16-lane) reductions: v_max/v_add with row_ror operands ---
+template <int kRor>
+__device__ __forceinline__ float row_ror(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + kRor, 0xF, 0xF,
+                                                               false));
+}
+__device__ __forceinline__ float row_max16(float v) {
+  v = fmaxf(v, row_ror<8>(v));
+  v = fmaxf(v, row_ror<4>(v));
+  v = fmaxf(v, row_ror<2>(v));
+  v = fmaxf(v, row_ror<1>(v));
+  return v;
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v += row_ror<8>(v);
+  v += row_ror<4>(v);
+  v += row_ror<2>(v);
+  v += row_ror<1>(v);
+  return v;
 }
 
 }  // namespace kvssd

@@ -184,9 +184,11 @@ int launch_typed(const GeneralParams& prm, dim3 grid, int bits, hipStream_t s) {
 }  // namespace
 
 SplitPlan plan_splits(const kvssd_decode_desc& d, int units) {
-  // about 2048 (kv head, split) work items: 8 waves per CU on a 256-CU part
-  // for the matrix-core kernel, 2048+ four-wave workgroups for the general one
-  long per = (static_cast<long>(units) * d.kv_heads + 2047) / 2048;
+  // about 1024 (kv head, split) work items: one resident round of the
+  // matrix-core kernel (4 single-wave workgroups per CU on a 256-CU part, each
+  // streaming its blocks with loads one sub-block ahead); the general kernel
+  // runs 1024+ four-wave workgroups
+  long per = (static_cast<long>(units) * d.kv_heads + 1023) / 1024;
   SplitPlan plan{};
   plan.blocks_per_split = static_cast<int>(per < 1 ? 1 : per);
   plan.splits = (units + plan.blocks_per_split - 1) / plan.blocks_per_split;

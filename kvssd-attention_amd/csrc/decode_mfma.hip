@@ -8,7 +8,8 @@
 // and shared by all its query heads.
 //
 // Code -> fp16 without a dequantised tensor: a code c placed in the mantissa of
-// 1.0 gives v = 1 + c/F (F = 2^bits, common.hpp), and (c - mid) = F (v - 1.5).
+// 1.0 gives v = 1 + c/F (F = 64 for INT4, 4 for INT2; common.hpp), and
+// (c - mid) = F (v - OFF) with OFF = 1 + mid/F.
 //
 // QK (v_mfma_f32_16x16x32_f16, 4 per 16-token tile and query quad):
 //   A = query, rows (h', g') = 4 heads x 4 groups, each row holding head h'
@@ -16,7 +17,7 @@
 //       tokens of the tile.  Lane l loads 16 B (INT4) / 8 B (INT2) of token
 //       l%16's row at chunk l/16, i.e. group l/16 of that token; MFMA m takes
 //       word m (INT4) / a half of word m/2 (INT2).  C starts at
-//       -1.5 * sum_{d in g'} q[h',d], so C[(h',g'),t] = sum_{d in g'} q (c-mid)/F.
+//       -OFF * sum_{d in g'} q[h',d], so C[(h',g'),t] = sum_{d in g'} q (c-mid)/F.
 //   Lane l ends with the 4 groups of head l/16, token l%16, and forms
 //   s = F * sm_scale * log2(e) * sum_g scale_k[t,g] * C[g] in registers.
 // softmax: exact per sub-block max (16-lane row reduction), running (m, l) in
@@ -29,7 +30,10 @@
 //   B = W, columns (h'', g'') = 4 heads x 4 groups: W[t,(h,g)] = p[h,t] *
 //       scale_v[t,g] in fp16, written by the QK lanes into LDS and read back
 //       16 B per lane.  Only the column whose group owns a tile's dims is kept;
-//       out = F * (C - 1.5 * sum_t W), the sum taken from the same fp16 W.
+//       out = F * (C - OFF * sum_t W), the sum taken from the same fp16 W.
+// Software pipelining: the next sub-block's loads (K, V, both scale rows) go
+// out into a second register stage before the current sub-block computes, so
+// every wave keeps ~18 KB in flight while its MFMAs and VALU run.
 // Token <-> MFMA K-slot map (shared by A and B): K step k, lane group q,
 //   slot s -> token 16*dimperm(s) + 4q + k, dimperm(s) = (s>>1) + 4(s&1)
 //   (the order the magic unpack leaves nibbles in).  The tr read row r of
@@ -53,6 +57,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kSub = 128;           // tokens per sub-block
 constexpr int kTiles = kSub / 16;   // QK tiles per sub-block
@@ -84,21 +89,6 @@ __device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
 }
 
-__device__ __forceinline__ float row_max16(float v) {
-  v = fmaxf(v, __shfl_xor(v, 8, kWave));
-  v = fmaxf(v, __shfl_xor(v, 4, kWave));
-  v = fmaxf(v, __shfl_xor(v, 2, kWave));
-  v = fmaxf(v, __shfl_xor(v, 1, kWave));
-  return v;
-}
-__device__ __forceinline__ float row_sum16(float v) {
-  v += __shfl_xor(v, 8, kWave);
-  v += __shfl_xor(v, 4, kWave);
-  v += __shfl_xor(v, 2, kWave);
-  v += __shfl_xor(v, 1, kWave);
-  return v;
-}
-
 // dim of MFMA m's slot s for lane group q (K operand of the QK product)
 template <int BITS>
 __device__ __forceinline__ int qk_dim(int m, int q, int s) {
@@ -126,18 +116,18 @@ __device__ __forceinline__ u32x4 k_operand(const u32x4& raw, int m) {
 // INT2 nibble-transposed word -> fp16 (row j, row j+4) pairs of one code lane
 // (parity 0: even dim, bits 4r..4r+1; parity 1: odd dim, bits 4r+2..4r+3).
 __device__ __forceinline__ u32x4 int2_tr_operand(uint32_t x, int parity) {
-  constexpr uint32_t m = 0x03000300u;
+  const uint32_t m = kMaskInt2;
   u32x4 out;
   if (parity == 0) {
-    out[0] = ((x << 8) & m) | kF16One2;
-    out[1] = ((x << 4) & m) | kF16One2;
-    out[2] = (x & m) | kF16One2;
-    out[3] = ((x >> 4) & m) | kF16One2;
+    out[0] = and_or(x << 8, m, kF16One2);
+    out[1] = and_or(x << 4, m, kF16One2);
+    out[2] = and_or(x, m, kF16One2);
+    out[3] = and_or(x >> 4, m, kF16One2);
   } else {
-    out[0] = ((x << 6) & m) | kF16One2;
-    out[1] = ((x << 2) & m) | kF16One2;
-    out[2] = ((x >> 2) & m) | kF16One2;
-    out[3] = ((x >> 6) & m) | kF16One2;
+    out[0] = and_or(x << 6, m, kF16One2);
+    out[1] = and_or(x << 2, m, kF16One2);
+    out[2] = and_or(x >> 2, m, kF16One2);
+    out[3] = and_or(x >> 6, m, kF16One2);
   }
   return out;
 }
@@ -155,12 +145,207 @@ __device__ __forceinline__ float query_at(const MfmaParams& p, int head, int d) 
   return load_query<QT>(p.query, head * 128 + d);
 }
 
+// ------------------------------------------------------------------ stages
+// Registers of one 128-token sub-block's loads (INT2 uses the first two words).
+struct Stage {
+  u32x4 k[kTiles], v[kTiles];
+  u32x2 sk[kTiles], sv[kTiles];
+};
+
+// Position in the wave's work: unit u (attended block), its block id, its
+// clamped valid count and the current sub-block start.
+struct Cursor {
+  int u, blk, vb, sb0;
+};
+
+// Advance to the next sub-block holding at least one valid token; false at the
+// end of the wave's units.  All values are wave-uniform.
+__device__ __forceinline__ bool next_sub(Cursor& c, const MfmaParams& p, int u_end) {
+  c.sb0 += kSub;
+  while (c.sb0 >= c.vb) {
+    if (++c.u >= u_end) return false;
+    const int blk = p.table ? p.table[c.u] : c.u;
+    c.blk = blk;
+    c.vb = (blk < 0 || blk >= p.num_blocks) ? 0 : clamp_valid(p.valid[blk], p.block_tokens);  // host-checked ids
+    c.sb0 = 0;
+  }
+  return true;
+}
+
+template <int BITS>
+__device__ __forceinline__ void issue_loads(Stage& st, const MfmaParams& p, const Cursor& c, int kvh, int li, int lq) {
+  constexpr int PD = 128 * BITS / 8;
+  const long tok0 = static_cast<long>(c.blk) * p.block_tokens + c.sb0;
+#pragma unroll
+  for (int tau = 0; tau < kTiles; ++tau) {
+    const long row = (tok0 + 16 * tau + li) * p.kv_heads + kvh;
+    if (BITS == 4) {
+      st.k[tau] = *reinterpret_cast<const u32x4*>(p.pk + row * PD + 16 * lq);
+      st.v[tau] = *reinterpret_cast<const u32x4*>(p.pv + row * PD + 16 * lq);
+    } else {
+      const u32x2 k2 = *reinterpret_cast<const u32x2*>(p.pk + row * PD + 8 * lq);
+      const u32x2 v2 = *reinterpret_cast<const u32x2*>(p.pv + row * PD + 8 * lq);
+      st.k[tau] = u32x4{k2[0], k2[1], 0u, 0u};
+      st.v[tau] = u32x4{v2[0], v2[1], 0u, 0u};
+    }
+    st.sk[tau] = *reinterpret_cast<const u32x2*>(p.sk + row * 4);
+    st.sv[tau] = *reinterpret_cast<const u32x2*>(p.sv + row * 4);
+  }
+}
+
+// Running state of one query quad.
+struct QuadState {
+  float m_run, l_run, wsum;
+  f32x4 acc[8];
+};
+
+template <int BITS, int QUADS, int QSPLIT>
+__device__ __forceinline__ void process(const Stage& st, const Cursor& c, uint8_t* v_lds, uint8_t* w_lds,
+                                        const u32x4 (&qa)[QUADS][QSPLIT][4], const f32x4 (&qcorr)[QUADS],
+                                        const float (&kscale)[QUADS], QuadState (&qs)[QUADS], int li, int lq) {
+  const half2_t ones2 = half2_t{static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  __syncthreads();  // the previous sub-block's LDS reads are done
+  // ------------------------------------------------------------ V rows -> LDS
+#pragma unroll
+  for (int tau = 0; tau < kTiles; ++tau) {
+    const int t = 16 * tau + li;
+    if (BITS == 4) {
+      const u32x4 v = st.v[tau];
+      const u32x4 w = (tau & 1) ? u32x4{v[2], v[3], v[0], v[1]} : v;
+      *reinterpret_cast<u32x4*>(v_lds + t * 64 + 16 * (lq ^ (tau >> 1))) = w;
+    } else {
+      const int r = (t & ~15) | ((t & 15) ^ tau);
+      const int pos = lq ^ (2 * (t & 1));
+      *reinterpret_cast<u32x2*>(v_lds + r * 32 + 8 * pos) = u32x2{st.v[tau][0], st.v[tau][1]};
+    }
+  }
+  // -------------------------------------------------------------------- QK
+  float score[QUADS][kTiles];
+#pragma unroll
+  for (int tau = 0; tau < kTiles; ++tau) {
+    u32x4 b[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) b[m] = k_operand<BITS>(st.k[tau], m);
+    const uint32_t s01 = st.sk[tau][0], s23 = st.sk[tau][1];
+    const float sk0 = half_bits_to_float(static_cast<uint16_t>(s01 & 0xFFFFu));
+    const float sk1 = half_bits_to_float(static_cast<uint16_t>(s01 >> 16));
+    const float sk2 = half_bits_to_float(static_cast<uint16_t>(s23 & 0xFFFFu));
+    const float sk3 = half_bits_to_float(static_cast<uint16_t>(s23 >> 16));
+    const bool ok = c.sb0 + 16 * tau + li < c.vb;
+#pragma unroll
+    for (int quad = 0; quad < QUADS; ++quad) {
+      f32x4 cc = qcorr[quad];
+#pragma unroll
+      for (int sp = 0; sp < QSPLIT; ++sp)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) cc = mfma16(qa[quad][sp][m], b[m], cc);
+      const float sc = (sk0 * cc[0] + sk1 * cc[1] + sk2 * cc[2] + sk3 * cc[3]) * kscale[quad];
+      score[quad][tau] = ok ? sc : -INFINITY;
+    }
+  }
+  // --------------------------------------------------------------- softmax
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    float mx = score[quad][0];
+#pragma unroll
+    for (int tau = 1; tau < kTiles; ++tau) mx = fmaxf(mx, score[quad][tau]);
+    mx = row_max16(mx);
+    const float m_new = fmaxf(qs[quad].m_run, mx);
+    const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(qs[quad].m_run - m_new);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    qs[quad].m_run = m_new;
+    float psum = 0.0f;
+    _Float16 w[4][kTiles];
+#pragma unroll
+    for (int tau = 0; tau < kTiles; ++tau) {
+      // masked tokens: score -inf gives p = 0, and their scales (possibly
+      // garbage padding) are replaced by 0 with a select, never a branch
+      const bool ok = score[quad][tau] != -INFINITY;
+      const float pr = __builtin_amdgcn_exp2f(score[quad][tau] - m_use);
+      psum += pr;
+      const uint32_t s01 = ok ? st.sv[tau][0] : 0u;
+      const uint32_t s23 = ok ? st.sv[tau][1] : 0u;
+      w[0][tau] = static_cast<_Float16>(pr * half_bits_to_float(static_cast<uint16_t>(s01 & 0xFFFFu)));
+      w[1][tau] = static_cast<_Float16>(pr * half_bits_to_float(static_cast<uint16_t>(s01 >> 16)));
+      w[2][tau] = static_cast<_Float16>(pr * half_bits_to_float(static_cast<uint16_t>(s23 & 0xFFFFu)));
+      w[3][tau] = static_cast<_Float16>(pr * half_bits_to_float(static_cast<uint16_t>(s23 >> 16)));
+    }
+    qs[quad].l_run = qs[quad].l_run * alpha + psum;
+    // W rows: slot 32*(t%4) + 8*(t/4) + s holds tile dimperm(s)
+    uint8_t* wbase = w_lds + quad * 16 * kWRow + (32 * (li & 3) + 8 * (li >> 2)) * 2;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const u32x4 v = u32x4{pack_half2(w[g][0], w[g][4]), pack_half2(w[g][1], w[g][5]), pack_half2(w[g][2], w[g][6]),
+                            pack_half2(w[g][3], w[g][7])};
+      *reinterpret_cast<u32x4*>(wbase + (lq * 4 + g) * kWRow) = v;
+    }
+    // rescale the PV state of column head li/4 by that head's alpha
+    const float a_pv = __shfl(alpha, (li >> 2) << 4, kWave);
+    if (__any(a_pv != 1.0f)) {
+      qs[quad].wsum *= a_pv;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) qs[quad].acc[n] *= a_pv;
+    }
+  }
+  __syncthreads();  // V and W tiles visible to every lane
+  // -------------------------------------------------------------------- PV
+#pragma unroll
+  for (int kp = 0; kp < 2; ++kp) {
+    u32x4 wb[QUADS][2];
+#pragma unroll
+    for (int quad = 0; quad < QUADS; ++quad)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int k = 2 * kp + kk;
+        wb[quad][kk] = *reinterpret_cast<const u32x4*>(w_lds + quad * 16 * kWRow + li * kWRow + (32 * k + 8 * lq) * 2);
+      }
+    // tr row of this lane: token 16*(r%8) + 4q + 2kp + r/8 with r = li
+    const int tt = 16 * (li & 7) + 4 * lq + 2 * kp + (li >> 3);
+    if (BITS == 4) {
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const i32x2 tr = lds_read_tr4(v_lds, tt * 64 + 8 * (n ^ (li & 7)));
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          uint32_t wv[4];
+          unpack_int4_f16(static_cast<uint32_t>(tr[kk]), wv);
+          const u32x4 a = u32x4{wv[0], wv[1], wv[2], wv[3]};
+#pragma unroll
+          for (int quad = 0; quad < QUADS; ++quad) qs[quad].acc[n] = mfma16(a, wb[quad][kk], qs[quad].acc[n]);
+        }
+      }
+    } else {
+      const int r = (tt & ~15) | ((tt & 15) ^ (tt >> 4));
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const i32x2 tr = lds_read_tr4(v_lds, r * 32 + 8 * (n ^ (2 * (li >> 3))));
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+          for (int par = 0; par < 2; ++par) {
+            const u32x4 a = int2_tr_operand(static_cast<uint32_t>(tr[kk]), par);
+#pragma unroll
+            for (int quad = 0; quad < QUADS; ++quad)
+              qs[quad].acc[2 * n + par] = mfma16(a, wb[quad][kk], qs[quad].acc[2 * n + par]);
+          }
+      }
+    }
+    // column sums of W over this lane's K slots (the fp16 values the MFMA saw)
+#pragma unroll
+    for (int quad = 0; quad < QUADS; ++quad)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          qs[quad].wsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, wb[quad][kk][j]), ones2, qs[quad].wsum, false);
+  }
+}
+
 template <int BITS, int QUADS, int QSPLIT, typename QT>
 __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
-  constexpr int PD = 128 * BITS / 8;  // bytes per (token, kv head) row
-  constexpr float F = static_cast<float>(1 << BITS);
-  constexpr int kTiles2 = 8;          // PV dim tiles (16 dims each)
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[kSub * PD];
+  constexpr float F = kUnpackScale<BITS>;
+  constexpr float OFF = kUnpackOffset<BITS>;
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds[kSub * 128 * BITS / 8];
   __shared__ __attribute__((aligned(16))) uint8_t w_lds[QUADS * 16 * kWRow];
 
   const int lane = threadIdx.x;
@@ -180,6 +365,13 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
   const int u_end = min(p.units, u_begin + p.blocks_per_split);
   const int head0 = kvh * p.gq;
 
+  // first sub-block's loads go out before the query set-up
+  Stage s0, s1;
+  Cursor cur{u_begin - 1, 0, 0, 0};
+  bool have0 = next_sub(cur, p, u_end);
+  Cursor c0 = cur;
+  if (have0) issue_loads<BITS>(s0, p, c0, kvh, li, lq);
+
   // ---------------------------------------------------------------- query
   u32x4 qa[QUADS][QSPLIT][4];
   f32x4 qcorr[QUADS];
@@ -188,13 +380,12 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
   for (int quad = 0; quad < QUADS; ++quad) {
     // per-head power-of-two normaliser (exact); fp16 queries are used as is
     const int hrow = quad * 4 + lq;  // head of this lane's QK row
+    const int hrow_c = hrow < p.gq ? hrow : p.gq - 1;
     float e_row = 0.0f;
     if (QSPLIT == 2) {
       float mx = 0.0f;
-      if (hrow < p.gq) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(query_at<QT>(p, head0 + hrow, 8 * li + i)));
-      }
+      for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(query_at<QT>(p, head0 + hrow_c, 8 * li + i)));
       mx = row_max16(mx);
       int ex = 0;
       if (mx > 0.0f && isfinite(mx)) {
@@ -206,6 +397,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
     kscale[quad] = F * p.scale_log2 * exp2f(e_row);
     // A operand: lane row (h', g') = (li/4, li%4), non-zero when g' == lane group
     const int ha = quad * 4 + (li >> 2);
+    const int ha_c = ha < p.gq ? ha : p.gq - 1;  // in-range head for unused rows
     const float e_a = __shfl(e_row, (li >> 2) << 4, kWave);
     const bool live = (li & 3) == lq && ha < p.gq;
 #pragma unroll
@@ -213,7 +405,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
       _Float16 hi[8], lo[8];
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
-        float x = live ? query_at<QT>(p, head0 + ha, qk_dim<BITS>(m, lq, s)) : 0.0f;
+        const float raw = query_at<QT>(p, head0 + ha_c, qk_dim<BITS>(m, lq, s));
+        float x = live ? raw : 0.0f;
         if (QSPLIT == 2) x = ldexpf(x, -static_cast<int>(e_a));
         hi[s] = static_cast<_Float16>(x);
         lo[s] = static_cast<_Float16>(x - static_cast<float>(hi[s]));
@@ -221,247 +414,99 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
       qa[quad][0][m] = u32x4{pack_half2(hi[0], hi[1]), pack_half2(hi[2], hi[3]), pack_half2(hi[4], hi[5]),
                              pack_half2(hi[6], hi[7])};
       if (QSPLIT == 2)
-        qa[quad][QSPLIT - 1][m] = u32x4{pack_half2(lo[0], lo[1]), pack_half2(lo[2], lo[3]),
-                                        pack_half2(lo[4], lo[5]), pack_half2(lo[6], lo[7])};
+        qa[quad][QSPLIT - 1][m] = u32x4{pack_half2(lo[0], lo[1]), pack_half2(lo[2], lo[3]), pack_half2(lo[4], lo[5]),
+                                        pack_half2(lo[6], lo[7])};
     }
-    // correction -1.5 * sum_{d in g} (hi + lo) for head hrow, all 4 groups:
+    // correction -OFF * sum_{d in g} (hi + lo) for head hrow, all 4 groups:
     // lane (row lq, li) sums dims 8li..8li+7 (group li/4); quads of lanes meet
     float part = 0.0f;
-    if (hrow < p.gq) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float x = query_at<QT>(p, head0 + hrow, 8 * li + i);
-        if (QSPLIT == 2) x = ldexpf(x, -static_cast<int>(e_row));
-        const _Float16 h16 = static_cast<_Float16>(x);
-        const float rep = QSPLIT == 2 ? static_cast<float>(h16) + static_cast<float>(static_cast<_Float16>(
-                                                                     x - static_cast<float>(h16)))
-                                      : static_cast<float>(h16);
-        part += rep;
-      }
+    for (int i = 0; i < 8; ++i) {
+      float x = query_at<QT>(p, head0 + hrow_c, 8 * li + i);
+      if (QSPLIT == 2) x = ldexpf(x, -static_cast<int>(e_row));
+      const _Float16 h16 = static_cast<_Float16>(x);
+      const float rep = QSPLIT == 2 ? static_cast<float>(h16) +
+                                          static_cast<float>(static_cast<_Float16>(x - static_cast<float>(h16)))
+                                    : static_cast<float>(h16);
+      part += rep;
     }
     part += __shfl_xor(part, 1, kWave);
     part += __shfl_xor(part, 2, kWave);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) qcorr[quad][g] = -1.5f * __shfl(part, (lq << 4) + 4 * g, kWave);
+    for (int g = 0; g < 4; ++g) qcorr[quad][g] = -OFF * __shfl(part, (lq << 4) + 4 * g, kWave);
   }
 
-  // ------------------------------------------------------------ accumulators
-  float m_run[QUADS], l_run[QUADS], wsum[QUADS];
-  f32x4 acc[QUADS][kTiles2];
+  QuadState qs[QUADS];
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
-    m_run[quad] = -INFINITY;
-    l_run[quad] = 0.0f;
-    wsum[quad] = 0.0f;
+    qs[quad].m_run = -INFINITY;
+    qs[quad].l_run = 0.0f;
+    qs[quad].wsum = 0.0f;
 #pragma unroll
-    for (int n = 0; n < kTiles2; ++n) acc[quad][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int n = 0; n < 8; ++n) qs[quad].acc[n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
-  for (int u = u_begin; u < u_end; ++u) {
-    const int blk = p.table ? p.table[u] : u;
-    if (blk < 0 || blk >= p.num_blocks) continue;  // ids are checked on the host
-    const int vb = clamp_valid(p.valid[blk], p.block_tokens);
-    for (int sb0 = 0; sb0 < vb; sb0 += kSub) {
-      const long tok0 = static_cast<long>(blk) * p.block_tokens + sb0;
-      // ---------------------------------------------------------- loads
-      u32x4 kraw[kTiles], vraw[kTiles];
-      u32x2 skr[kTiles], svr[kTiles];
-#pragma unroll
-      for (int tau = 0; tau < kTiles; ++tau) {
-        const long row = (tok0 + 16 * tau + li) * p.kv_heads + kvh;
-        if (BITS == 4) {
-          kraw[tau] = *reinterpret_cast<const u32x4*>(p.pk + row * PD + 16 * lq);
-          vraw[tau] = *reinterpret_cast<const u32x4*>(p.pv + row * PD + 16 * lq);
-        } else {
-          const u32x2 k2 = *reinterpret_cast<const u32x2*>(p.pk + row * PD + 8 * lq);
-          const u32x2 v2 = *reinterpret_cast<const u32x2*>(p.pv + row * PD + 8 * lq);
-          kraw[tau] = u32x4{k2[0], k2[1], 0u, 0u};
-          vraw[tau] = u32x4{v2[0], v2[1], 0u, 0u};
-        }
-        skr[tau] = *reinterpret_cast<const u32x2*>(p.sk + row * 4);
-        svr[tau] = *reinterpret_cast<const u32x2*>(p.sv + row * 4);
-      }
-      __syncthreads();  // previous sub-block's LDS reads are done
-      // ------------------------------------------------- V rows -> LDS
-#pragma unroll
-      for (int tau = 0; tau < kTiles; ++tau) {
-        const int t = 16 * tau + li;
-        if (BITS == 4) {
-          const u32x4 v = vraw[tau];
-          const u32x4 w = (tau & 1) ? u32x4{v[2], v[3], v[0], v[1]} : v;
-          *reinterpret_cast<u32x4*>(v_lds + t * 64 + 16 * (lq ^ (tau >> 1))) = w;
-        } else {
-          const int r = (t & ~15) | ((t & 15) ^ tau);
-          const int pos = lq ^ (2 * (t & 1));
-          *reinterpret_cast<u32x2*>(v_lds + r * 32 + 8 * pos) = u32x2{vraw[tau][0], vraw[tau][1]};
-        }
-      }
-      // -------------------------------------------------------------- QK
-      float score[QUADS][kTiles];
-#pragma unroll
-      for (int tau = 0; tau < kTiles; ++tau) {
-        u32x4 b[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) b[m] = k_operand<BITS>(kraw[tau], m);
-        const uint32_t s01 = skr[tau][0], s23 = skr[tau][1];
-        const float sk0 = half_bits_to_float(static_cast<uint16_t>(s01 & 0xFFFFu));
-        const float sk1 = half_bits_to_float(static_cast<uint16_t>(s01 >> 16));
-        const float sk2 = half_bits_to_float(static_cast<uint16_t>(s23 & 0xFFFFu));
-        const float sk3 = half_bits_to_float(static_cast<uint16_t>(s23 >> 16));
-        const bool ok = sb0 + 16 * tau + li < vb;
-#pragma unroll
-        for (int quad = 0; quad < QUADS; ++quad) {
-          f32x4 c = qcorr[quad];
-#pragma unroll
-          for (int sp = 0; sp < QSPLIT; ++sp)
-#pragma unroll
-            for (int m = 0; m < 4; ++m) c = mfma16(qa[quad][sp][m], b[m], c);
-          const float s = (sk0 * c[0] + sk1 * c[1] + sk2 * c[2] + sk3 * c[3]) * kscale[quad];
-          score[quad][tau] = ok ? s : -INFINITY;
-        }
-      }
-      // --------------------------------------------------------- softmax
-#pragma unroll
-      for (int quad = 0; quad < QUADS; ++quad) {
-        float mx = score[quad][0];
-#pragma unroll
-        for (int tau = 1; tau < kTiles; ++tau) mx = fmaxf(mx, score[quad][tau]);
-        mx = row_max16(mx);
-        const float m_new = fmaxf(m_run[quad], mx);
-        const float alpha = m_new == -INFINITY ? 1.0f : exp2f(m_run[quad] - m_new);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        m_run[quad] = m_new;
-        float psum = 0.0f;
-        _Float16 w[4][kTiles];
-#pragma unroll
-        for (int tau = 0; tau < kTiles; ++tau) {
-          const bool ok = score[quad][tau] != -INFINITY;
-          const float pr = ok ? exp2f(score[quad][tau] - m_use) : 0.0f;
-          psum += pr;
-          const uint32_t s01 = svr[tau][0], s23 = svr[tau][1];
-          w[0][tau] = static_cast<_Float16>(ok ? pr * half_bits_to_float(static_cast<uint16_t>(s01 & 0xFFFFu)) : 0.0f);
-          w[1][tau] = static_cast<_Float16>(ok ? pr * half_bits_to_float(static_cast<uint16_t>(s01 >> 16)) : 0.0f);
-          w[2][tau] = static_cast<_Float16>(ok ? pr * half_bits_to_float(static_cast<uint16_t>(s23 & 0xFFFFu)) : 0.0f);
-          w[3][tau] = static_cast<_Float16>(ok ? pr * half_bits_to_float(static_cast<uint16_t>(s23 >> 16)) : 0.0f);
-        }
-        l_run[quad] = l_run[quad] * alpha + psum;
-        // W rows: slot 32*(t%4) + 8*(t/4) + s holds tile dimperm(s)
-        uint8_t* wbase = w_lds + quad * 16 * kWRow + (32 * (li & 3) + 8 * (li >> 2)) * 2;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const u32x4 v = u32x4{pack_half2(w[g][0], w[g][4]), pack_half2(w[g][1], w[g][5]),
-                                pack_half2(w[g][2], w[g][6]), pack_half2(w[g][3], w[g][7])};
-          *reinterpret_cast<u32x4*>(wbase + (lq * 4 + g) * kWRow) = v;
-        }
-        // rescale the PV state of column head li/4 by that head's alpha
-        const float a_pv = __shfl(alpha, (li >> 2) << 4, kWave);
-        if (__any(a_pv != 1.0f)) {
-          wsum[quad] *= a_pv;
-#pragma unroll
-          for (int n = 0; n < kTiles2; ++n) acc[quad][n] *= a_pv;
-        }
-      }
-      __syncthreads();  // V and W tiles visible to every lane
-      // -------------------------------------------------------------- PV
-#pragma unroll
-      for (int kp = 0; kp < 2; ++kp) {
-        u32x4 wb[QUADS][2];
-#pragma unroll
-        for (int quad = 0; quad < QUADS; ++quad)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            const int k = 2 * kp + kk;
-            wb[quad][kk] =
-                *reinterpret_cast<const u32x4*>(w_lds + quad * 16 * kWRow + li * kWRow + (32 * k + 8 * lq) * 2);
-          }
-        // tr row of this lane: token 16*(r%8) + 4q + 2kp + r/8 with r = li
-        const int tt = 16 * (li & 7) + 4 * lq + 2 * kp + (li >> 3);
-        if (BITS == 4) {
-#pragma unroll
-          for (int n = 0; n < 8; ++n) {
-            const int off = tt * 64 + 8 * (n ^ (li & 7));
-            const i32x2 tr = lds_read_tr4(v_lds, off);
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-              uint32_t wv[4];
-              unpack_int4_f16(static_cast<uint32_t>(tr[kk]), wv);
-              const u32x4 a = u32x4{wv[0], wv[1], wv[2], wv[3]};
-#pragma unroll
-              for (int quad = 0; quad < QUADS; ++quad) acc[quad][n] = mfma16(a, wb[quad][kk], acc[quad][n]);
-            }
-          }
-        } else {
-          const int r = (tt & ~15) | ((tt & 15) ^ (tt >> 4));
-#pragma unroll
-          for (int n = 0; n < 4; ++n) {
-            const int off = r * 32 + 8 * (n ^ (2 * (li >> 3)));
-            const i32x2 tr = lds_read_tr4(v_lds, off);
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-              for (int par = 0; par < 2; ++par) {
-                const u32x4 a = int2_tr_operand(static_cast<uint32_t>(tr[kk]), par);
-#pragma unroll
-                for (int quad = 0; quad < QUADS; ++quad)
-                  acc[quad][2 * n + par] = mfma16(a, wb[quad][kk], acc[quad][2 * n + par]);
-              }
-          }
-        }
-        // column sums of W over this lane's K slots (same fp16 values the MFMA saw)
-#pragma unroll
-        for (int quad = 0; quad < QUADS; ++quad)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const uint32_t x = wb[quad][kk][j];
-              wsum[quad] += half_bits_to_float(static_cast<uint16_t>(x & 0xFFFFu)) +
-                            half_bits_to_float(static_cast<uint16_t>(x >> 16));
-            }
-      }
-    }
+  // ------------------------------------------- software-pipelined main loop
+  // stage s0 computes while stage s1's loads are in flight, then swap
+  while (have0) {
+    const bool have1 = next_sub(cur, p, u_end);
+    const Cursor c1 = cur;
+    if (have1) issue_loads<BITS>(s1, p, c1, kvh, li, lq);
+    process<BITS, QUADS, QSPLIT>(s0, c0, v_lds, w_lds, qa, qcorr, kscale, qs, li, lq);
+    if (!have1) break;
+    have0 = next_sub(cur, p, u_end);
+    c0 = cur;
+    if (have0) issue_loads<BITS>(s0, p, c0, kvh, li, lq);
+    process<BITS, QUADS, QSPLIT>(s1, c1, v_lds, w_lds, qa, qcorr, kscale, qs, li, lq);
   }
 
   // ----------------------------------------------------------------- epilogue
   const long prow = static_cast<long>(split) * p.query_heads + head0;
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
-    const float l_tot = row_sum16(l_run[quad]);
-    float wtot = wsum[quad];
+    const float l_tot = row_sum16(qs[quad].l_run);
+    float wtot = qs[quad].wsum;
     wtot += __shfl_xor(wtot, 16, kWave);
     wtot += __shfl_xor(wtot, 32, kWave);
     const int hrow = quad * 4 + lq;
     if (li == 0 && hrow < p.gq) {
-      p.part_ml[2 * (prow + hrow)] = m_run[quad];
+      p.part_ml[2 * (prow + hrow)] = qs[quad].m_run;
       p.part_ml[2 * (prow + hrow) + 1] = l_tot;
     }
     const int hcol = quad * 4 + (li >> 2);
     const int g = li & 3;
     if (hcol < p.gq) {
       float* orow = p.part_o + (prow + hcol) * 128;
+      // out = F * (C - OFF * sum W) on the tiles whose dims lie in group g;
+      // compile-time tile indices keep the accumulators in registers
       if (BITS == 4) {
 #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int n = 2 * g + half;
-          const f32x4 c = acc[quad][n];
-          f32x4 o;
+        for (int n = 0; n < 8; ++n) {
+          if ((n >> 1) == g) {
+            f32x4 o;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o[i] = F * (c[i] - 1.5f * wtot);
-          *reinterpret_cast<f32x4*>(orow + 16 * n + 4 * lq) = o;
+            for (int i = 0; i < 4; ++i) o[i] = F * (qs[quad].acc[n][i] - OFF * wtot);
+            *reinterpret_cast<f32x4*>(orow + 16 * n + 4 * lq) = o;
+          }
         }
       } else {
-        const f32x4 ev = acc[quad][2 * g], od = acc[quad][2 * g + 1];
-        f32x4 o0, o1;
-        o0[0] = F * (ev[0] - 1.5f * wtot);
-        o0[1] = F * (od[0] - 1.5f * wtot);
-        o0[2] = F * (ev[1] - 1.5f * wtot);
-        o0[3] = F * (od[1] - 1.5f * wtot);
-        o1[0] = F * (ev[2] - 1.5f * wtot);
-        o1[1] = F * (od[2] - 1.5f * wtot);
-        o1[2] = F * (ev[3] - 1.5f * wtot);
-        o1[3] = F * (od[3] - 1.5f * wtot);
-        *reinterpret_cast<f32x4*>(orow + 32 * g + 8 * lq) = o0;
-        *reinterpret_cast<f32x4*>(orow + 32 * g + 8 * lq + 4) = o1;
+#pragma unroll
+        for (int gg = 0; gg < 4; ++gg) {
+          if (gg == g) {
+            const f32x4 ev = qs[quad].acc[2 * gg], od = qs[quad].acc[2 * gg + 1];
+            f32x4 o0, o1;
+            o0[0] = F * (ev[0] - OFF * wtot);
+            o0[1] = F * (od[0] - OFF * wtot);
+            o0[2] = F * (ev[1] - OFF * wtot);
+            o0[3] = F * (od[1] - OFF * wtot);
+            o1[0] = F * (ev[2] - OFF * wtot);
+            o1[1] = F * (od[2] - OFF * wtot);
+            o1[2] = F * (ev[3] - OFF * wtot);
+            o1[3] = F * (od[3] - OFF * wtot);
+            *reinterpret_cast<f32x4*>(orow + 32 * gg + 8 * lq) = o0;
+            *reinterpret_cast<f32x4*>(orow + 32 * gg + 8 * lq + 4) = o1;
+          }
+        }
       }
     }
   }

@@ -19,6 +19,14 @@ namespace {
 constexpr int kMergeThreads = 256;
 constexpr int kMaxSplitWeights = 4096;
 
+// One workgroup per (query head, 32-dim slice).  Phase 1 reduces the global
+// max and normaliser over the splits (one split per lane, strided); phase 2
+// gives each of the 8 waves' lane groups 32 dims and every 8th split, so each
+// load instruction reads 128 contiguous bytes of one split's row, and the 8
+// partial sums meet in LDS.
+constexpr int kSliceDims = 32;
+constexpr int kPhases = kMergeThreads / kSliceDims;  // 8
+
 __global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(const float* __restrict__ part_o,
                                                                      const float* __restrict__ part_ml, int splits,
                                                                      int query_heads, int head_dim,
@@ -26,7 +34,9 @@ __global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(const float
   __shared__ float weight[kMaxSplitWeights];
   __shared__ float red[kMergeThreads / kWave];
   __shared__ float bcast[2];
+  __shared__ float partial[kPhases][kSliceDims];
   const int h = blockIdx.x;
+  const int d0 = blockIdx.y * kSliceDims;
   const int tid = threadIdx.x;
 
   // 1) global max over non-empty splits
@@ -46,13 +56,13 @@ __global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(const float
   __syncthreads();
   const float big_m = bcast[0];
 
-  // 2) per-split weights and the total normaliser
+  // 2) per-split weights 2^(m_s - M) and the total normaliser
   float lsum = 0.0f;
   for (int s = tid; s < splits; s += kMergeThreads) {
     const long r = static_cast<long>(s) * query_heads + h;
     const float l = part_ml[2 * r + 1];
     const float w = (l > 0.0f) ? exp2f(part_ml[2 * r] - big_m) : 0.0f;
-    if (s < kMaxSplitWeights) weight[s] = w;
+    weight[s] = w;  // splits <= kMaxSplitWeights is checked on the host
     lsum += w * l;
   }
   lsum = wave_sum(lsum);
@@ -66,25 +76,26 @@ __global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(const float
   }
   __syncthreads();
   const float big_l = bcast[1];
-  const float inv_l = big_l > 0.0f ? 1.0f / big_l : 0.0f;
 
-  // 3) weighted sum of the unnormalised outputs
-  for (int dd = tid; dd < head_dim; dd += kMergeThreads) {
-    float acc = 0.0f;
-    for (int s = 0; s < splits; ++s) {
-      const long r = static_cast<long>(s) * query_heads + h;
-      float w;
-      if (s < kMaxSplitWeights) {
-        w = weight[s];
-      } else {
-        const float l = part_ml[2 * r + 1];
-        w = (l > 0.0f) ? exp2f(part_ml[2 * r] - big_m) : 0.0f;
-      }
-      if (w != 0.0f) acc += w * part_o[r * head_dim + dd];
+  // 3) weighted sum of the unnormalised outputs of this 32-dim slice
+  const int dd = tid % kSliceDims;
+  const int ph = tid / kSliceDims;
+  float acc = 0.0f;
+  if (d0 + dd < head_dim) {
+    for (int s = ph; s < splits; s += kPhases) {
+      const float w = weight[s];
+      if (w != 0.0f) acc += w * part_o[(static_cast<long>(s) * query_heads + h) * head_dim + d0 + dd];
     }
-    out[static_cast<long>(h) * head_dim + dd] = acc * inv_l;
   }
-  if (tid == 0) lse[h] = big_l > 0.0f ? kLn2 * (big_m + log2f(big_l)) : -INFINITY;
+  partial[ph][dd] = acc;
+  __syncthreads();
+  if (tid < kSliceDims && d0 + tid < head_dim) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int q = 0; q < kPhases; ++q) sum += partial[q][tid];
+    out[static_cast<long>(h) * head_dim + d0 + tid] = big_l > 0.0f ? sum / big_l : 0.0f;
+  }
+  if (tid == 0 && blockIdx.y == 0) lse[h] = big_l > 0.0f ? kLn2 * (big_m + log2f(big_l)) : -INFINITY;
 }
 
 __global__ __launch_bounds__(kMergeThreads) void merge_chunks_kernel(int dim, float* __restrict__ acc_out,
@@ -117,8 +128,10 @@ __global__ __launch_bounds__(kMergeThreads) void merge_chunks_kernel(int dim, fl
 
 int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, float* out, float* lse,
                         hipStream_t stream) {
-  hipLaunchKernelGGL(merge_splits_kernel, dim3(query_heads), dim3(kMergeThreads), 0, stream, parts.o, parts.ml,
-                     splits, query_heads, head_dim, out, lse);
+  if (splits > kMaxSplitWeights) return arg_error("too many splits for the merge kernel");
+  const int slices = (head_dim + kSliceDims - 1) / kSliceDims;
+  hipLaunchKernelGGL(merge_splits_kernel, dim3(query_heads, slices), dim3(kMergeThreads), 0, stream, parts.o,
+                     parts.ml, splits, query_heads, head_dim, out, lse);
   return hip_status(hipGetLastError(), "merge_splits launch");
 }
 
