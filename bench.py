@@ -111,6 +111,26 @@ def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 20.0
     }
 
 
+def copy_calibration(torch, dev, nbytes: int, steps: int, warmup: int) -> int:
+    """Plain device-to-device copy of a known size: its FETCH_SIZE / WRITE_SIZE
+    per dispatch, against nbytes, gives the counters' scale on this GPU."""
+    src = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    print(json.dumps({"copy_bytes": nbytes, "steps": steps, "ms_per_copy": round(ms, 5),
+                      "read_GBps": round(nbytes / ms / 1e6, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -120,11 +140,19 @@ def main() -> int:
     ap.add_argument("--kernel", default="auto", choices=["auto", "general", "mfma"])
     ap.add_argument("--copies", type=int, default=0, help="distinct KV copies rotated across steps (0 = auto)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument(
+        "--copy-calibration",
+        type=int,
+        default=0,
+        metavar="BYTES",
+        help="instead of decoding, time a plain device copy of BYTES bytes per step (the reference "
+        "reading for scaling rocprof FETCH_SIZE / WRITE_SIZE to bytes)",
+    )
     args = ap.parse_args()
     if args.gpus != 1:
         print(
             "bench.py measures one GPU only: this build has no multi-GPU path "
-            "(the decode shards by kv head or by token range across GPUs; see DESIGN.md)",
+            "(the decode would shard by kv head or by token range across GPUs)",
             file=sys.stderr,
         )
         return 2
@@ -137,6 +165,8 @@ def main() -> int:
     from kvssd.selectors import RecentSinkBlocks
 
     dev = torch.device("cuda", 0)
+    if args.copy_calibration:
+        return copy_calibration(torch, dev, args.copy_calibration, args.steps, args.warmup)
     tokens, bits, qh, vscale, outl, sel = WORKLOADS[args.workload]
     query, cache, valid = make_cache(torch, dev, tokens, bits, qh, vscale, outl)
     nb = tokens // BLOCK_TOKENS

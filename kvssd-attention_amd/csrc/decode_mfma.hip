@@ -203,7 +203,6 @@ template <int BITS, int QUADS, int QSPLIT>
 __device__ __forceinline__ void process(const Stage& st, const Cursor& c, uint8_t* v_lds, uint8_t* w_lds,
                                         const u32x4 (&qa)[QUADS][QSPLIT][4], const f32x4 (&qcorr)[QUADS],
                                         const float (&kscale)[QUADS], QuadState (&qs)[QUADS], int li, int lq) {
-  const half2_t ones2 = half2_t{static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
   __syncthreads();  // the previous sub-block's LDS reads are done
   // ------------------------------------------------------------ V rows -> LDS
 #pragma unroll
@@ -330,14 +329,19 @@ __device__ __forceinline__ void process(const Stage& st, const Cursor& c, uint8_
           }
       }
     }
-    // column sums of W over this lane's K slots (the fp16 values the MFMA saw)
+    // column sums of W over this lane's K slots (the fp16 values the MFMA saw);
+    // plain converts and adds: v_dot2c_f32_f16 against (1, 1) returned wrong
+    // sums in testing, so it is not used here
 #pragma unroll
     for (int quad = 0; quad < QUADS; ++quad)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          qs[quad].wsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(half2_t, wb[quad][kk][j]), ones2, qs[quad].wsum, false);
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t x = wb[quad][kk][j];
+          qs[quad].wsum += half_bits_to_float(static_cast<uint16_t>(x & 0xFFFFu)) +
+                           half_bits_to_float(static_cast<uint16_t>(x >> 16));
+        }
   }
 }
 
