@@ -115,16 +115,11 @@ constexpr float kUnpackScale = BITS == 4 ? 64.0f : 4.0f;     // F
 template <int BITS>
 constexpr float kUnpackOffset = BITS == 4 ? 1.125f : 1.5f;  // 1 + mid/F
 
-// (x & m) | c in one v_and_or_b32.  The backend splits this pattern into an
-// AND and an OR with literal operands (gfx9 allows one scalar/literal operand
-// per VALU instruction), so it is spelled out: m travels in a VGPR, c in an
-// SGPR.  Pure function (no side effects), so the compiler may still schedule,
-// hoist and CSE it.
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "s"(c));
-  return r;
-}
+// (x & m) | c.  Plain C on purpose: the backend emits v_and_b32 + v_or_b32
+// for it, and an inline-asm v_and_or_b32 is invisible to the compiler's hazard
+// recognizer, so a VALU result feeding an MFMA operand could be read without
+// the wait states the hardware needs (that produced wrong MFMA results here).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
 
 __device__ __forceinline__ void unpack_int4_f16(uint32_t x, uint32_t w[4]) {
   const uint32_t m = kMaskInt4;
