@@ -36,6 +36,11 @@ bool mfma_supported(const kvssd_decode_desc& d, std::string* why);
 bool mfma_aligned(const DecodeArgs& a);
 int launch_mfma(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts);
 
+// ---- LDS-staged matrix-core kernel: the matrix-core shapes with kv_heads % 4 == 0
+bool staged_supported(const kvssd_decode_desc& d, std::string* why);
+bool staged_aligned(const DecodeArgs& a);
+int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts);
+
 // ---- split-K phase 2: merge the partials of every split into (out, lse)
 int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, float* out, float* lse,
                         hipStream_t stream);

@@ -1,0 +1,783 @@
+// LDS-staged matrix-core decode kernel for gfx950: head_dim 128, group_size 32,
+// INT4 or INT2 codes, kv_heads % 4 == 0, at most 8 query heads per kv head,
+// block_tokens % 128 == 0.
+//
+// Same semantics as the general kernel (ReferenceAttentionBackend.run,
+// src/kvssd/backends/reference.py:22-50; element addressing of
+// csrc/fused_decode.cu:50-56).
+//
+// Work split.  A workgroup of 8 waves owns 4 consecutive kv heads (a "group")
+// and one split (a range of attended blocks).  It walks the split in stages of
+// 128 tokens; wave (w, half) computes kv head w of the group over tokens
+// 64*half .. 64*half+63 of every stage, and the two halves meet in LDS at the
+// end, so each workgroup writes one partial per query head of its group.
+//
+// Staging.  The packed rows of 4 kv heads of one token are contiguous in HBM
+// ([blocks][tokens][kv_heads][packed]), so a stage is four contiguous streams
+// (K codes, V codes, K scales, V scales).  They are copied HBM -> LDS with
+// global_load_lds_dwordx4 (16 bytes per lane, 1 KB per instruction, no VGPRs
+// held while in flight), double-buffered: stage i+1's copies are issued right
+// after the barrier that opens stage i, so they overlap all of stage i's math.
+// LDS per stage: 72 KB (INT4) / 40 KB (INT2), i.e. 144 KB / 80 KB in total.
+//
+// LDS layout.  A region stores, per token t of the stage, CPT 16-byte chunks
+// (CPT = 4 kv heads x packed bytes / 16); chunk idx of token t sits at
+// position t*CPT + (idx ^ phi(t)).  phi is chosen so that the matrix-core
+// operand reads below hit 16 distinct bank groups per 16 lanes; the DMA lane
+// -> global address map applies the inverse, so each copy instruction still
+// reads whole 128-byte lines of one contiguous HBM range.
+//
+// Code -> fp16 without a dequantised tensor: a code c in the mantissa of an
+// fp16 whose exponent is that of 1.0 reads as v = 1 + c/F, and
+// (c - mid) = F (v - OFF) with OFF = 1 + mid/F (F = 64 for INT4; 4 or 16 per
+// slot for INT2, absorbed by the query operand in QK and by the output factor
+// in PV).  The offset is removed through the accumulator: QK starts from
+// -sum q' OFF, PV subtracts an extra MFMA of W against OFF.
+//
+// QK (v_mfma_f32_16x16x32_f16): A = query, rows (h, g) = 4 heads x 4 groups,
+//   row (h, g) holding head h masked to group g; B = K codes of a 16-token
+//   tile.  Lane (li, lq) ends with the 4 group partials of head lq, token li,
+//   and forms s = sum_g scale_k[t, g] * C[g] with fp16-operand FMAs.
+// softmax: per-stage max by 16-lane DPP reduction, running (m, l) in log2
+//   units, p = 2^(s - m).  W[t, (h, g)] = p * scale_v[t, g] in fp16,
+//   written to LDS.
+// PV (v_mfma_f32_16x16x32_f16): A = V^T codes from a 16x16 nibble transpose
+//   read (ds_read_b64_tr_b4) of the staged V rows: one transpose read covers
+//   all 64 tokens of a wave's half for 16 dims (INT4) / 32 dims (INT2).
+//   B = W, columns (h, g); only the column whose group owns a tile's dims is
+//   kept.
+// Token <-> MFMA K slot (PV, shared by A and B): K step kk, lane group q,
+//   slot s -> token 16*(s&3) + 4q + 2kk + (s>>2) of the half; QK tile tau,
+//   lane li -> token 16*tau + li.  W of QK lane li, tile tau lives in slot
+//   4*u + tau of its (h, g) row, u = 8((li>>1)&1) + 2(li>>2) + (li&1).
+#include "decode.hpp"
+
+namespace kvssd {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kKG = 4;               // kv heads per workgroup
+constexpr int kWaves = 2 * kKG;      // (kv head, token half)
+constexpr int kThreads = 64 * kWaves;
+constexpr int kStageTok = 128;       // tokens per stage
+constexpr int kHalfTok = 64;         // tokens per wave per stage
+constexpr int kMaxUnits = 2048;      // attended blocks per split (block list kept in LDS)
+
+template <int BITS>
+struct Geo {
+  static constexpr int PD = 128 * BITS / 8;               // packed bytes per kv-head row
+  static constexpr int CPT = kKG * PD / 16;               // chunks per token row of the group
+  static constexpr int KV_BYTES = kStageTok * kKG * PD;   // one code region
+  static constexpr int SC_BYTES = kStageTok * kKG * 8;    // one scale region
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = KV_BYTES;
+  static constexpr int SK_OFF = 2 * KV_BYTES;
+  static constexpr int SV_OFF = 2 * KV_BYTES + SC_BYTES;
+  static constexpr int STAGE = 2 * KV_BYTES + 2 * SC_BYTES;
+  static constexpr int KV_INST = KV_BYTES / 1024;         // copy instructions per code region
+  static constexpr int SC_INST = SC_BYTES / 1024;         // ... per scale region
+  static constexpr int KV_PER_WAVE = KV_INST / kWaves;
+  // INT4: W lives in the wave's own (already consumed) K chunks of the stage;
+  // INT2 K chunks are too few for two query quads, so W gets its own region.
+  static constexpr bool W_IN_K = BITS == 4;
+};
+static_assert(Geo<4>::SC_INST * 2 == kWaves && Geo<2>::SC_INST * 2 == kWaves, "one scale copy per wave");
+
+struct StagedParams {
+  const void* query;
+  const uint8_t* pk;
+  const uint8_t* pv;
+  const uint8_t* sk;  // fp16 scales as bytes
+  const uint8_t* sv;
+  const int32_t* valid;
+  const int32_t* table;
+  float* part_o;
+  float* part_ml;
+  int query_heads, kv_heads, block_tokens, num_blocks, units, splits, blocks_per_split, gq;
+  float scale_log2;  // sm_scale * log2(e)
+};
+
+// ------------------------------------------------------------ small helpers
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c, 0,
+                                                0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+}
+
+__device__ __forceinline__ float half_lo(uint32_t x) { return half_bits_to_float(static_cast<uint16_t>(x & 0xFFFFu)); }
+__device__ __forceinline__ float half_hi(uint32_t x) { return half_bits_to_float(static_cast<uint16_t>(x >> 16)); }
+
+// XOR swizzle of a region's chunk index for token t (CPT chunks per token).
+template <int CPT>
+__device__ __forceinline__ int phi(int t) {
+  if constexpr (CPT == 16) return (t & 15) ^ (((t >> 4) & 3) << 2);
+  else if constexpr (CPT == 8) return ((t & 15) >> 1) ^ (((t >> 4) & 3) << 1);
+  else return (t >> 3) & 1;  // CPT == 2: scale rows
+}
+
+template <int CPT>
+__device__ __forceinline__ int chunk_byte(int t, int idx) {
+  return 16 * (t * CPT + (idx ^ phi<CPT>(t)));
+}
+
+// LDS byte address of a pointer into a __shared__ array
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)p));
+}
+
+// ds_read_b64_tr_b4 pairs (offsets 0 and 8 of each address): within each group
+// of 16 lanes, lane j receives nibble j of the 8 bytes every lane of the group
+// addressed, lane r's nibble landing in bits 4r..4r+3 (a 16x16 nibble
+// transpose).  Issued from asm, with its own lgkmcnt wait before the results
+// are handed back: the compiler's intrinsic form of this read carries no
+// memory operand, so the compiler would make it wait for every outstanding
+// global->LDS copy, i.e. for the next stage's prefetch.
+__device__ __forceinline__ void tr4_pairs4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, i32x2 (&r)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b4 %0, %8\n\t"
+      "ds_read_b64_tr_b4 %1, %8 offset:8\n\t"
+      "ds_read_b64_tr_b4 %2, %9\n\t"
+      "ds_read_b64_tr_b4 %3, %9 offset:8\n\t"
+      "ds_read_b64_tr_b4 %4, %10\n\t"
+      "ds_read_b64_tr_b4 %5, %10 offset:8\n\t"
+      "ds_read_b64_tr_b4 %6, %11\n\t"
+      "ds_read_b64_tr_b4 %7, %11 offset:8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
+      : "memory");
+}
+__device__ __forceinline__ void tr4_pairs2(uint32_t a0, uint32_t a1, i32x2 (&r)[4]) {
+  asm volatile(
+      "ds_read_b64_tr_b4 %0, %4\n\t"
+      "ds_read_b64_tr_b4 %1, %4 offset:8\n\t"
+      "ds_read_b64_tr_b4 %2, %5\n\t"
+      "ds_read_b64_tr_b4 %3, %5 offset:8\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+      : "v"(a0), "v"(a1)
+      : "memory");
+}
+
+__device__ __forceinline__ void dma16(const uint8_t* src, uint8_t* lds_dst) {
+  __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (lds_void_t*)(lds_dst), 16, 0, 0);
+}
+
+// ---------------------------------------------------------- code -> fp16 ---
+//
+// A code c placed at bit b (b + width <= 10) of an fp16 whose exponent field
+// is that of 1.0 reads as v = 1 + c/F with F = 2^(10 - b), and
+// (c - mid) = F (v - OFF), OFF = 1 + mid/F.  Codes go to the top mantissa bits
+// (F = 64 for INT4, 4 or 16 for INT2) so that the sums of v keep the bits the
+// result needs.  (Codes left in place as fp16 subnormals would save shifts,
+// but the matrix core does not multiply subnormal operands exactly against
+// operands of wide exponent range.)  One shift per distinct distance plus one
+// AND-OR per fp16 pair; the masks live in VGPRs so the backend can fuse AND +
+// OR into v_and_or_b32 (it may read only one scalar operand).
+struct Masks {
+  uint32_t m47;  // bits 4-7 of both halves (INT4, F = 64)
+  uint32_t m89;  // bits 8-9 (INT2, F = 4)
+  uint32_t m67;  // bits 6-7 (INT2, F = 16)
+};
+
+__device__ __forceinline__ Masks make_masks(uint32_t opaque_zero) {
+  return Masks{0x00F000F0u | opaque_zero, 0x03000300u | opaque_zero, 0x00C000C0u | opaque_zero};
+}
+
+__device__ __forceinline__ uint32_t ao(uint32_t x, uint32_t m) { return (x & m) | kF16One2; }
+
+// INT4 word x (nibbles n0..n7, n_i at bits 4i): fp16 slots s0..s7 hold
+// n0, n4, n1, n5, n2, n6, n3, n7 (slot s <-> nibble (s>>1) + 4(s&1)), F = 64.
+// The same routine serves K rows (nibble = dim) and transpose-read V words
+// (nibble = token row).
+__device__ __forceinline__ u32x4 unpack4(uint32_t x, const Masks& k) {
+  return u32x4{ao(x << 4, k.m47), ao(x, k.m47), ao(x >> 4, k.m47), ao(x >> 8, k.m47)};
+}
+
+// INT2 K word x (codes c0..c15, c_j at bits 2j): pairs (c_j, c_{j+8}) for
+// j = o..o+3 (o = 0 or 4); slot s = 2i + hi holds c_{o+i+8hi}.  Even j go to
+// bits 8-9 (F = 4), odd j to bits 6-7 (F = 16): F(s) = (s & 2) ? 16 : 4.
+__device__ __forceinline__ u32x4 unpack2(uint32_t x, int o, const Masks& k) {
+  if (o == 0) return u32x4{ao(x << 8, k.m89), ao(x << 4, k.m67), ao(x << 4, k.m89), ao(x, k.m67)};
+  return u32x4{ao(x, k.m89), ao(x >> 4, k.m67), ao(x >> 4, k.m89), ao(x >> 8, k.m67)};
+}
+
+// INT2 transpose-read word x (nibble rho = codes of dims 2j, 2j+1 of token
+// row rho): parity 0 takes the even-dim code (bits 4rho..4rho+1) to bits 8-9
+// (F = 4), parity 1 the odd one (bits 4rho+2..4rho+3) to bits 6-7 (F = 16);
+// slot s <-> row (s>>1) + 4(s&1).
+__device__ __forceinline__ u32x4 unpack2_tr(uint32_t x, int parity, const Masks& k) {
+  if (parity == 0) return u32x4{ao(x << 8, k.m89), ao(x << 4, k.m89), ao(x, k.m89), ao(x >> 4, k.m89)};
+  return u32x4{ao(x << 4, k.m67), ao(x, k.m67), ao(x >> 4, k.m67), ao(x >> 8, k.m67)};
+}
+
+// QK: the query operand of K slot s carries F(s) / G, so every product is
+// q * v(s) * F(s) / G, and the accumulator starts at -sum q' OFF(s);
+// then C = sum q (c - mid) / G.
+template <int BITS>
+constexpr float kQkG = BITS == 4 ? 64.0f : 4.0f;
+template <int BITS>
+__device__ __forceinline__ float qk_factor(int s) {
+  if (BITS == 4) return 1.0f;
+  return (s & 2) ? 4.0f : 1.0f;
+}
+template <int BITS>
+__device__ __forceinline__ float qk_off(int s) {
+  if (BITS == 4) return 1.125f;
+  return (s & 2) ? 1.125f : 1.5f;
+}
+
+// dim of QK MFMA m's slot s for lane group q
+template <int BITS>
+__device__ __forceinline__ int qk_dim(int m, int q, int s) {
+  if (BITS == 4) return 32 * q + 8 * m + (s >> 1) + 4 * (s & 1);
+  return 32 * q + 16 * (m >> 1) + 4 * (m & 1) + (s >> 1) + 8 * (s & 1);
+}
+
+// PV: V codes sit at one position per output tile (INT4: F = 64; INT2 parity
+// 0: F = 4, parity 1: F = 16), so out = F (C - sum_t W OFF); the correction
+// operand holds OFF in every slot (rows identical).
+__device__ __forceinline__ u32x4 off_operand(float off) {
+  const _Float16 h = static_cast<_Float16>(off);
+  const uint32_t w = pack_half2(h, h);
+  return u32x4{w, w, w, w};
+}
+
+// ---------------------------------------------------------------- cursor ---
+struct Cursor {
+  int u, blk, vb, sb0;
+};
+
+// Advance to the next stage holding at least one valid token; false at the
+// end of the split.  units[2i] / units[2i+1] = block id / clamped valid count
+// of the split's i-th attended block (LDS).  Wave-uniform.
+__device__ __forceinline__ bool next_stage(Cursor& c, const int* units, int n_units) {
+  c.sb0 += kStageTok;
+  while (c.sb0 >= c.vb) {
+    if (++c.u >= n_units) return false;
+    c.blk = __builtin_amdgcn_readfirstlane(units[2 * c.u]);
+    c.vb = __builtin_amdgcn_readfirstlane(units[2 * c.u + 1]);
+    c.sb0 = 0;
+  }
+  return true;
+}
+
+// Per-lane byte offsets (relative to the stage's group base) of this wave's
+// copy instructions: code regions (same map for K and V) and one scale copy.
+template <int BITS>
+struct CopyMap {
+  uint32_t kv[Geo<BITS>::KV_PER_WAVE];
+  uint32_t sc;
+};
+
+template <int BITS>
+__device__ __forceinline__ CopyMap<BITS> make_copy_map(int wave, int lane, int kv_heads) {
+  using G = Geo<BITS>;
+  CopyMap<BITS> cm;
+  const int rs = kv_heads * G::PD;
+#pragma unroll
+  for (int j = 0; j < G::KV_PER_WAVE; ++j) {
+    const int pos = 64 * (wave + kWaves * j) + lane;
+    const int t = pos / G::CPT, slot = pos % G::CPT;
+    cm.kv[j] = static_cast<uint32_t>(t * rs + 16 * (slot ^ phi<G::CPT>(t)));
+  }
+  const int pos = 64 * (wave & 3) + lane;
+  const int t = pos >> 1, slot = pos & 1;
+  cm.sc = static_cast<uint32_t>(t * kv_heads * 8 + 16 * (slot ^ phi<2>(t)));
+  return cm;
+}
+
+template <int BITS>
+__device__ __forceinline__ void issue_stage(const StagedParams& p, uint8_t* buf, const Cursor& c, int kvh0, int wave,
+                                            const CopyMap<BITS>& cm) {
+  using G = Geo<BITS>;
+  const long row0 = (static_cast<long>(c.blk) * p.block_tokens + c.sb0) * p.kv_heads + kvh0;
+  const uint8_t* kb = p.pk + row0 * G::PD;
+  const uint8_t* vb = p.pv + row0 * G::PD;
+#pragma unroll
+  for (int j = 0; j < G::KV_PER_WAVE; ++j) {
+    const int i = wave + kWaves * j;
+    dma16(kb + cm.kv[j], buf + G::K_OFF + 1024 * i);
+    dma16(vb + cm.kv[j], buf + G::V_OFF + 1024 * i);
+  }
+  const uint8_t* sb = (wave < 4 ? p.sk : p.sv) + row0 * 8;
+  dma16(sb + cm.sc, buf + (wave < 4 ? G::SK_OFF : G::SV_OFF) + 1024 * (wave & 3));
+}
+
+// W chunk (quad, row R = 4h + g, chunk c of 8 slots) byte offset.
+template <int BITS, int QUADS>
+__device__ __forceinline__ int w_chunk(int quad, int R, int c, int w, int half) {
+  if constexpr (Geo<BITS>::W_IN_K) {
+    // inside the wave's K chunks (kv head w, tokens of its half) of the stage
+    const int b = c >> 2;
+    const int t = kHalfTok * half + 32 * quad + (R & 7) + 8 * ((R >> 3) ^ b) + 16 * b;
+    return Geo<BITS>::K_OFF + chunk_byte<16>(t, 4 * w + (c & 3));
+  } else {
+    // own region after both stage buffers, [wave][quad][row][8 chunks]
+    const int rp = R ^ ((R >> 2) & 1);
+    return quad * 2048 + rp * 128 + 16 * (c ^ ((rp >> 1) & 7));
+  }
+}
+
+// ----------------------------------------------------------- query set-up ---
+template <int QUADS, int QSPLIT>
+struct QueryOps {
+  u32x4 qa[QUADS][QSPLIT][4];
+  f32x4 qcorr[QUADS];
+  float kscale[QUADS];
+};
+
+template <int BITS, int QUADS, int QSPLIT, typename QT>
+__device__ __forceinline__ void setup_query(QueryOps<QUADS, QSPLIT>& qo, const StagedParams& p, int head0, int li,
+                                            int lq) {
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    // per-head power-of-two normaliser (exact): |q| * 2^-e in [1, 2)
+    const int hrow = quad * 4 + lq;
+    const int hrow_c = hrow < p.gq ? hrow : p.gq - 1;
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(load_query<QT>(p.query, (head0 + hrow_c) * 128 + 8 * li + i)));
+    mx = row_max16(mx);
+    int ex = 0;
+    if (mx > 0.0f && isfinite(mx)) {
+      frexpf(mx, &ex);
+      ex -= 1;
+    }
+    qo.kscale[quad] = kQkG<BITS> * p.scale_log2 * exp2f(static_cast<float>(ex));
+    // A operand: lane row (h', g') = (li/4, li%4), non-zero when g' == lane group
+    const int ha = quad * 4 + (li >> 2);
+    const int ha_c = ha < p.gq ? ha : p.gq - 1;
+    const int e_a = __shfl(ex, (li >> 2) << 4, kWave);
+    const bool live = (li & 3) == lq && ha < p.gq;
+    float part = 0.0f;  // sum over this lane's row entries of (hi + lo) * OFF
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      _Float16 hi[8], lo[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float raw = load_query<QT>(p.query, (head0 + ha_c) * 128 + qk_dim<BITS>(m, lq, s));
+        const float x = live ? ldexpf(raw, -e_a) * qk_factor<BITS>(s) : 0.0f;
+        hi[s] = static_cast<_Float16>(x);
+        lo[s] = QSPLIT == 2 ? static_cast<_Float16>(x - static_cast<float>(hi[s])) : static_cast<_Float16>(0.0f);
+        part += (static_cast<float>(hi[s]) + static_cast<float>(lo[s])) * qk_off<BITS>(s);
+      }
+      qo.qa[quad][0][m] = u32x4{pack_half2(hi[0], hi[1]), pack_half2(hi[2], hi[3]), pack_half2(hi[4], hi[5]),
+                                pack_half2(hi[6], hi[7])};
+      if (QSPLIT == 2)
+        qo.qa[quad][QSPLIT - 1][m] = u32x4{pack_half2(lo[0], lo[1]), pack_half2(lo[2], lo[3]),
+                                           pack_half2(lo[4], lo[5]), pack_half2(lo[6], lo[7])};
+    }
+    // C init of lane (li, lq), register g: row (h = lq, g) -> the lane holding
+    // that A row's non-zero entries is (li = 4 lq + g, group g)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) qo.qcorr[quad][g] = -__shfl(part, 16 * g + 4 * lq + g, kWave);
+  }
+}
+
+// ---------------------------------------------------------- per-wave state ---
+template <int BITS, int QUADS>
+struct WaveState {
+  float m_run[QUADS], l_run[QUADS];
+  f32x4 acc[QUADS][8];
+  f32x4 corr[QUADS][BITS == 4 ? 1 : 2];
+};
+
+// One stage of one wave: tokens 64*half .. 64*half + hv - 1 of the stage are valid.
+template <int BITS, int QUADS, int QSPLIT>
+__device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase, int hv, int w, int half, int li,
+                                              int lq, const Masks& mk, const QueryOps<QUADS, QSPLIT>& qo,
+                                              const u32x4 (&offa)[BITS == 4 ? 1 : 2], WaveState<BITS, QUADS>& st) {
+  using G = Geo<BITS>;
+  // ---------------------------------------------------------------- QK
+  float score[QUADS][4];
+  u32x2 svw[4];
+#pragma unroll
+  for (int tau = 0; tau < 4; ++tau) {
+    const int t = kHalfTok * half + 16 * tau + li;
+    u32x4 b[4];
+    if (BITS == 4) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(buf + G::K_OFF + chunk_byte<16>(t, 4 * w + lq));
+#pragma unroll
+      for (int m = 0; m < 4; ++m) b[m] = unpack4(raw[m], mk);
+    } else {
+      const u32x2 raw =
+          *reinterpret_cast<const u32x2*>(buf + G::K_OFF + chunk_byte<8>(t, 2 * w + (lq >> 1)) + 8 * (lq & 1));
+#pragma unroll
+      for (int m = 0; m < 4; ++m) b[m] = unpack2(raw[m >> 1], m & 1, mk);
+    }
+    const int sbyte = chunk_byte<2>(t, w >> 1) + 8 * (w & 1);
+    const u32x2 skw = *reinterpret_cast<const u32x2*>(buf + G::SK_OFF + sbyte);
+    svw[tau] = *reinterpret_cast<const u32x2*>(buf + G::SV_OFF + sbyte);
+    const bool ok = 16 * tau + li < hv;
+#pragma unroll
+    for (int quad = 0; quad < QUADS; ++quad) {
+      f32x4 cc = qo.qcorr[quad];
+#pragma unroll
+      for (int sp = 0; sp < QSPLIT; ++sp)
+#pragma unroll
+        for (int m = 0; m < 4; ++m) cc = mfma16(qo.qa[quad][sp][m], b[m], cc);
+      float raw = __builtin_fmaf(half_lo(skw[0]), cc[0], 0.0f);
+      raw = __builtin_fmaf(half_hi(skw[0]), cc[1], raw);
+      raw = __builtin_fmaf(half_lo(skw[1]), cc[2], raw);
+      raw = __builtin_fmaf(half_hi(skw[1]), cc[3], raw);
+      score[quad][tau] = ok ? raw * qo.kscale[quad] : -INFINITY;
+    }
+  }
+  // unit of this lane's W slots (4 tiles) in its (h, g) rows
+  const int u = 8 * ((li >> 1) & 1) + 2 * (li >> 2) + (li & 1);
+  // --------------------------------------------------------------- softmax
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    float mx = fmaxf(fmaxf(score[quad][0], score[quad][1]), fmaxf(score[quad][2], score[quad][3]));
+    mx = row_max16(mx);
+    const float m_new = fmaxf(st.m_run[quad], mx);
+    const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m_run[quad] - m_new);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    st.m_run[quad] = m_new;
+    float pr[4];
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau) pr[tau] = __builtin_amdgcn_exp2f(score[quad][tau] - m_use);
+    st.l_run[quad] = st.l_run[quad] * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+    // W = p * scale_v in fp16, masked tokens carry scale 0
+    uint32_t wlo[4], whi[4];  // per group g: (tile 0, tile 1), (tile 2, tile 3)
+#pragma unroll
+    for (int tau = 0; tau < 4; tau += 2) {
+      const bool ok0 = score[quad][tau] != -INFINITY;
+      const bool ok1 = score[quad][tau + 1] != -INFINITY;
+      const float p0 = pr[tau], p1 = pr[tau + 1];
+      const uint32_t a01 = ok0 ? svw[tau][0] : 0u, a23 = ok0 ? svw[tau][1] : 0u;
+      const uint32_t b01 = ok1 ? svw[tau + 1][0] : 0u, b23 = ok1 ? svw[tau + 1][1] : 0u;
+      const uint32_t w0 = pack_half2(static_cast<_Float16>(p0 * half_lo(a01)), static_cast<_Float16>(p1 * half_lo(b01)));
+      const uint32_t w1 = pack_half2(static_cast<_Float16>(p0 * half_hi(a01)), static_cast<_Float16>(p1 * half_hi(b01)));
+      const uint32_t w2 = pack_half2(static_cast<_Float16>(p0 * half_lo(a23)), static_cast<_Float16>(p1 * half_lo(b23)));
+      const uint32_t w3 = pack_half2(static_cast<_Float16>(p0 * half_hi(a23)), static_cast<_Float16>(p1 * half_hi(b23)));
+      if (tau == 0) {
+        wlo[0] = w0; wlo[1] = w1; wlo[2] = w2; wlo[3] = w3;
+      } else {
+        whi[0] = w0; whi[1] = w1; whi[2] = w2; whi[3] = w3;
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int off = w_chunk<BITS, QUADS>(quad, 4 * lq + g, u >> 1, w, half) + 8 * (u & 1);
+      *reinterpret_cast<u32x2*>(wbase + off) = u32x2{wlo[g], whi[g]};
+    }
+    // rescale the PV state of column head li/4 by that head's alpha
+    const float a_pv = __shfl(alpha, (li >> 2) << 4, kWave);
+    if (__any(a_pv != 1.0f)) {
+#pragma unroll
+      for (int n = 0; n < 8; ++n) st.acc[quad][n] *= a_pv;
+#pragma unroll
+      for (int c = 0; c < (BITS == 4 ? 1 : 2); ++c) st.corr[quad][c] *= a_pv;
+    }
+  }
+  // -------------------------------------------------------------------- PV
+  u32x4 wb[QUADS][2];
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      wb[quad][kk] = *reinterpret_cast<const u32x4*>(wbase + w_chunk<BITS, QUADS>(quad, li, 4 * kk + lq, w, half));
+  // transpose-read row of this lane: kk = li >> 3, row rho = li & 7,
+  // slot s = 2(rho & 3) + (rho >> 2) -> token 16(s&3) + 4lq + 2kk + (s>>2)
+  const int rho = li & 7;
+  const int s_tr = ((rho & 3) << 1) | (rho >> 2);
+  const int t_tr = kHalfTok * half + 16 * (s_tr & 3) + 4 * lq + 2 * (li >> 3) + (s_tr >> 2);
+  const uint32_t vbase = lds_addr(buf + G::V_OFF);
+  if (BITS == 4) {
+    i32x2 trs[8];
+    tr4_pairs4(vbase + chunk_byte<16>(t_tr, 4 * w), vbase + chunk_byte<16>(t_tr, 4 * w + 1),
+               vbase + chunk_byte<16>(t_tr, 4 * w + 2), vbase + chunk_byte<16>(t_tr, 4 * w + 3), trs);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      const i32x2 tr = trs[n];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const u32x4 a = unpack4(static_cast<uint32_t>(tr[kk]), mk);
+#pragma unroll
+        for (int quad = 0; quad < QUADS; ++quad) st.acc[quad][n] = mfma16(a, wb[quad][kk], st.acc[quad][n]);
+      }
+    }
+  } else {
+    i32x2 trs[4];
+    tr4_pairs2(vbase + chunk_byte<8>(t_tr, 2 * w), vbase + chunk_byte<8>(t_tr, 2 * w + 1), trs);
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const i32x2 tr = trs[n];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int par = 0; par < 2; ++par) {
+          const u32x4 a = unpack2_tr(static_cast<uint32_t>(tr[kk]), par, mk);
+#pragma unroll
+          for (int quad = 0; quad < QUADS; ++quad)
+            st.acc[quad][2 * n + par] = mfma16(a, wb[quad][kk], st.acc[quad][2 * n + par]);
+        }
+    }
+  }
+  // sum over tokens of W * OFF per column, through the matrix core
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int c = 0; c < (BITS == 4 ? 1 : 2); ++c) st.corr[quad][c] = mfma16(offa[c], wb[quad][kk], st.corr[quad][c]);
+}
+
+template <int BITS, int QUADS, int QSPLIT, typename QT>
+__global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p) {
+  using G = Geo<BITS>;
+  constexpr int kWBytes = G::W_IN_K ? 0 : kWaves * QUADS * 2048;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * G::STAGE + kWBytes + kMaxUnits * 8];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int w = wave & (kKG - 1);
+  const int half = wave / kKG;
+  const int li = lane & 15;
+  const int lq = lane >> 4;
+
+  // workgroup -> (split, group of 4 kv heads); the two groups of a split read
+  // the two halves of the same token rows at about the same time
+  const int groups = p.kv_heads / kKG;
+  const int grp = blockIdx.x % groups;
+  const int split = blockIdx.x / groups;
+  const int u_begin = split * p.blocks_per_split;
+  const int u_end = min(p.units, u_begin + p.blocks_per_split);
+  const int kvh0 = grp * kKG;
+  const int head0 = (kvh0 + w) * p.gq;
+
+  // the split's (block id, clamped valid count) list, read once into LDS
+  int* units = reinterpret_cast<int*>(lds + 2 * G::STAGE + kWBytes);
+  const int n_units = max(0, u_end - u_begin);  // <= kMaxUnits, checked on the host
+  for (int i = threadIdx.x; i < n_units; i += kThreads) {
+    const int blk = p.table ? p.table[u_begin + i] : u_begin + i;
+    units[2 * i] = blk;
+    units[2 * i + 1] = (blk < 0 || blk >= p.num_blocks) ? 0 : clamp_valid(p.valid[blk], p.block_tokens);
+  }
+  __syncthreads();
+
+  const CopyMap<BITS> cm = make_copy_map<BITS>(wave, lane, p.kv_heads);
+  Cursor cur{-1, 0, 0, -kStageTok};
+  bool have = next_stage(cur, units, n_units);
+  if (have) issue_stage<BITS>(p, lds, cur, kvh0, wave, cm);
+
+  QueryOps<QUADS, QSPLIT> qo;
+  setup_query<BITS, QUADS, QSPLIT, QT>(qo, p, head0, li, lq);
+  // masks in VGPRs: p.units >= 1, so (lane & (p.units >> 30)) is 0 but opaque
+  const Masks mk = make_masks(static_cast<uint32_t>(lane) & static_cast<uint32_t>(p.units >> 30));
+  u32x4 offa[BITS == 4 ? 1 : 2];
+  if (BITS == 4) {
+    offa[0] = off_operand(1.125f);
+  } else {
+    offa[0] = off_operand(1.5f);
+    offa[BITS == 4 ? 0 : 1] = off_operand(1.125f);
+  }
+
+  WaveState<BITS, QUADS> st;
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    st.m_run[quad] = -INFINITY;
+    st.l_run[quad] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) st.acc[quad][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < (BITS == 4 ? 1 : 2); ++c) st.corr[quad][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+
+  // ------------------------------------------- double-buffered stage loop
+  int buf = 0;
+  while (have) {
+    const Cursor c0 = cur;
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
+    __syncthreads();                     // ... everyone's; and the other buffer is free
+    have = next_stage(cur, units, n_units);
+    if (have) issue_stage<BITS>(p, lds + (buf ^ 1) * G::STAGE, cur, kvh0, wave, cm);
+    const int hv = min(kStageTok, c0.vb - c0.sb0) - kHalfTok * half;
+    if (hv > 0) {
+      uint8_t* sbuf = lds + buf * G::STAGE;
+      uint8_t* wbase = G::W_IN_K ? sbuf : lds + 2 * G::STAGE + wave * QUADS * 2048;
+      compute_stage<BITS, QUADS, QSPLIT>(sbuf, wbase, hv, w, half, li, lq, mk, qo, offa, st);
+    }
+    buf ^= 1;
+  }
+
+  // -------------------------------------------------------------- epilogue
+  // out = F (C - corr) per column: F = 64 (INT2 parity 0: 4, parity 1: 16)
+  // lane (li, lq): column (head li/4, group li%4), rows = dims of its tiles
+  float* xo = reinterpret_cast<float*>(lds);  // [w][quad][lane][8] from half 1
+  float* xm = xo + kKG * QUADS * 64 * 8;      // [w][quad][4 heads][2]
+  __syncthreads();  // every wave is done with the stage buffers
+  float ov[QUADS][8];
+  float mh[QUADS], lh[QUADS];
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    const int g = li & 3;
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+      if (gg == g) {
+        if (BITS == 4) {
+          const float cr = st.corr[quad][0][0];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            ov[quad][i] = 64.0f * (st.acc[quad][2 * gg][i] - cr);
+            ov[quad][4 + i] = 64.0f * (st.acc[quad][2 * gg + 1][i] - cr);
+          }
+        } else {
+          const float c0 = st.corr[quad][0][0], c1 = st.corr[quad][BITS == 4 ? 0 : 1][0];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            ov[quad][i] = 4.0f * (st.acc[quad][2 * gg][i] - c0);
+            ov[quad][4 + i] = 16.0f * (st.acc[quad][2 * gg + 1][i] - c1);
+          }
+        }
+      }
+    }
+    // (m, l) of head li/4 (the QK layout keeps head lq in lanes 16lq..16lq+15)
+    const float l_tot = row_sum16(st.l_run[quad]);
+    mh[quad] = __shfl(st.m_run[quad], (li >> 2) << 4, kWave);
+    lh[quad] = __shfl(l_tot, (li >> 2) << 4, kWave);
+    if (half == 1) {
+      float* dst = xo + ((w * QUADS + quad) * 64 + lane) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dst[i] = ov[quad][i];
+      if (lq == 0 && (li & 3) == 0) {
+        xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2] = mh[quad];
+        xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2 + 1] = lh[quad];
+      }
+    }
+  }
+  __syncthreads();
+  if (half == 1) return;
+  const long prow = static_cast<long>(split) * p.query_heads + head0;
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    const float* src = xo + ((w * QUADS + quad) * 64 + lane) * 8;
+    const float mb = xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2];
+    const float lb = xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2 + 1];
+    const float ma = mh[quad], la = lh[quad];
+    const float mm = fmaxf(ma, mb);
+    const float wa = (la > 0.0f) ? exp2f(ma - mm) : 0.0f;
+    const float wb2 = (lb > 0.0f) ? exp2f(mb - mm) : 0.0f;
+    const float lt = la * wa + lb * wb2;
+    const int hcol = quad * 4 + (li >> 2);
+    if (hcol < p.gq) {
+      float* orow = p.part_o + (prow + hcol) * 128;
+      const int g = li & 3;
+      f32x4 o0, o1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o0[i] = (wa != 0.0f ? wa * ov[quad][i] : 0.0f) + (wb2 != 0.0f ? wb2 * src[i] : 0.0f);
+        o1[i] = (wa != 0.0f ? wa * ov[quad][4 + i] : 0.0f) + (wb2 != 0.0f ? wb2 * src[4 + i] : 0.0f);
+      }
+      if (BITS == 4) {
+        // tiles 2g, 2g+1: dims 16n + 4lq + i
+        *reinterpret_cast<f32x4*>(orow + 32 * g + 4 * lq) = o0;
+        *reinterpret_cast<f32x4*>(orow + 32 * g + 16 + 4 * lq) = o1;
+      } else {
+        // tile 2g + par: dims 32g + 2(4lq + i) + par
+        f32x4 e0, e1;
+        e0[0] = o0[0]; e0[1] = o1[0]; e0[2] = o0[1]; e0[3] = o1[1];
+        e1[0] = o0[2]; e1[1] = o1[2]; e1[2] = o0[3]; e1[3] = o1[3];
+        *reinterpret_cast<f32x4*>(orow + 32 * g + 8 * lq) = e0;
+        *reinterpret_cast<f32x4*>(orow + 32 * g + 8 * lq + 4) = e1;
+      }
+      if (lq == 0 && g == 0) {
+        p.part_ml[2 * (prow + hcol)] = lt > 0.0f ? mm : -INFINITY;
+        p.part_ml[2 * (prow + hcol) + 1] = lt;
+      }
+    }
+  }
+}
+
+template <int BITS, int QUADS, int QSPLIT, typename QT>
+void launch_one(const StagedParams& prm, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((decode_staged_kernel<BITS, QUADS, QSPLIT, QT>), dim3(grid), dim3(kThreads), 0, s, prm);
+}
+
+template <int BITS, int QUADS>
+int launch_quads(const StagedParams& prm, int grid, int dtype, hipStream_t s) {
+  switch (dtype) {
+    case KVSSD_DTYPE_F16:
+      launch_one<BITS, QUADS, 1, _Float16>(prm, grid, s);
+      break;
+    case KVSSD_DTYPE_BF16:
+      launch_one<BITS, QUADS, 2, uint16_t>(prm, grid, s);
+      break;
+    case KVSSD_DTYPE_F32:
+      launch_one<BITS, QUADS, 2, float>(prm, grid, s);
+      break;
+    case KVSSD_DTYPE_F64:
+      launch_one<BITS, QUADS, 2, double>(prm, grid, s);
+      break;
+    default:
+      return arg_error("unsupported query dtype");
+  }
+  return hip_status(hipGetLastError(), "decode_staged launch");
+}
+
+}  // namespace
+
+bool staged_supported(const kvssd_decode_desc& d, std::string* why) {
+  auto no = [&](const char* r) {
+    if (why) *why = r;
+    return false;
+  };
+  if (d.head_dim != 128) return no("head_dim must be 128");
+  if (d.group_size != 32) return no("group_size must be 32");
+  if (d.block_tokens % kStageTok) return no("block_tokens must be a multiple of 128");
+  if (d.kv_heads % kKG) return no("kv_heads must be a multiple of 4");
+  const int units = d.num_selected > 0 ? d.num_selected : d.num_blocks;
+  if (plan_splits(d, units).blocks_per_split > kMaxUnits) return no("too many blocks per split");
+  const int gq = d.query_heads / d.kv_heads;
+  if (gq < 1 || gq > 8) return no("at most 8 query heads per kv head");
+  return true;
+}
+
+bool staged_aligned(const DecodeArgs& a) {
+  auto ok = [&](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) % 16) == 0; };
+  return ok(a.packed_k) && ok(a.packed_v) && ok(a.scales_k) && ok(a.scales_v);
+}
+
+int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts) {
+  const kvssd_decode_desc& d = a.desc;
+  StagedParams prm{};
+  prm.query = a.query;
+  prm.pk = a.packed_k;
+  prm.pv = a.packed_v;
+  prm.sk = reinterpret_cast<const uint8_t*>(a.scales_k);
+  prm.sv = reinterpret_cast<const uint8_t*>(a.scales_v);
+  prm.valid = a.valid;
+  prm.table = a.table;
+  prm.part_o = parts.o;
+  prm.part_ml = parts.ml;
+  prm.query_heads = d.query_heads;
+  prm.kv_heads = d.kv_heads;
+  prm.block_tokens = d.block_tokens;
+  prm.num_blocks = d.num_blocks;
+  prm.units = a.units;
+  prm.splits = plan.splits;
+  prm.blocks_per_split = plan.blocks_per_split;
+  prm.gq = d.query_heads / d.kv_heads;
+  prm.scale_log2 = static_cast<float>(d.sm_scale) * kLog2e;
+  const int grid = plan.splits * (d.kv_heads / kKG);
+  const bool two = prm.gq > 4;
+  if (d.bits == 4) return two ? launch_quads<4, 2>(prm, grid, d.query_dtype, a.stream)
+                              : launch_quads<4, 1>(prm, grid, d.query_dtype, a.stream);
+  return two ? launch_quads<2, 2>(prm, grid, d.query_dtype, a.stream)
+             : launch_quads<2, 1>(prm, grid, d.query_dtype, a.stream);
+}
+
+}  // namespace kvssd

@@ -3,7 +3,9 @@
 // merge_splits: split-K phase 2.  For query head h with split partials
 // (O_s unnormalised, m_s in log2 units, l_s = sum 2^(s - m_s)):
 //   M = max_s m_s,  L = sum_s l_s 2^(m_s - M),
-//   out = sum_s O_s 2^(m_s - M) / L,  lse = ln 2 * (M + log2 L).
+//   out = sum_s O_s 2^(m_s - M) / L,  lse = ln 2 * (M + log2 L),
+// evaluated as a running fold (m, l, o) <- (max, rescaled sums), which gives
+// the same M and the same terms.
 // Splits with l_s = 0 (no valid token) contribute nothing; if every split is
 // empty, out = 0 and lse = -inf (attention over an empty token set, as
 // src/kvssd/backends/reference.py:46-49 returns it).
@@ -17,85 +19,66 @@ namespace kvssd {
 namespace {
 
 constexpr int kMergeThreads = 256;
-constexpr int kMaxSplitWeights = 4096;
 
-// One workgroup per (query head, 32-dim slice).  Phase 1 reduces the global
-// max and normaliser over the splits (one split per lane, strided); phase 2
-// gives each of the 8 waves' lane groups 32 dims and every 8th split, so each
-// load instruction reads 128 contiguous bytes of one split's row, and the 8
-// partial sums meet in LDS.
+// One workgroup per (query head, 32-dim slice); thread (phase, dim) folds the
+// splits s = phase (mod 8) into a running (m, l, o) with the online rescaling
+// (loads 16 splits at a time so their latencies overlap), then the 8 phases
+// meet in LDS.  One pass over the partials, no second round trip for the
+// global max.
 constexpr int kSliceDims = 32;
 constexpr int kPhases = kMergeThreads / kSliceDims;  // 8
+constexpr int kBatch = 16;
+
+__device__ __forceinline__ void fold(float& m, float& l, float& o, float ms, float ls, float os) {
+  if (ls > 0.0f) {
+    const float mn = fmaxf(m, ms);
+    const float a = exp2f(m - mn);  // m = -inf on the first fold: a = 0
+    const float b = exp2f(ms - mn);
+    o = o * a + os * b;
+    l = l * a + ls * b;
+    m = mn;
+  }
+}
 
 __global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(const float* __restrict__ part_o,
                                                                      const float* __restrict__ part_ml, int splits,
                                                                      int query_heads, int head_dim,
                                                                      float* __restrict__ out, float* __restrict__ lse) {
-  __shared__ float weight[kMaxSplitWeights];
-  __shared__ float red[kMergeThreads / kWave];
-  __shared__ float bcast[2];
-  __shared__ float partial[kPhases][kSliceDims];
+  __shared__ float sm[kPhases][kSliceDims], sl[kPhases][kSliceDims], so[kPhases][kSliceDims];
   const int h = blockIdx.x;
   const int d0 = blockIdx.y * kSliceDims;
-  const int tid = threadIdx.x;
-
-  // 1) global max over non-empty splits
-  float mx = -INFINITY;
-  for (int s = tid; s < splits; s += kMergeThreads) {
-    const long r = static_cast<long>(s) * query_heads + h;
-    if (part_ml[2 * r + 1] > 0.0f) mx = fmaxf(mx, part_ml[2 * r]);
-  }
-  mx = wave_max(mx);
-  if (tid % kWave == 0) red[tid / kWave] = mx;
-  __syncthreads();
-  if (tid == 0) {
-    float m = red[0];
-    for (int w = 1; w < kMergeThreads / kWave; ++w) m = fmaxf(m, red[w]);
-    bcast[0] = m;
-  }
-  __syncthreads();
-  const float big_m = bcast[0];
-
-  // 2) per-split weights 2^(m_s - M) and the total normaliser
-  float lsum = 0.0f;
-  for (int s = tid; s < splits; s += kMergeThreads) {
-    const long r = static_cast<long>(s) * query_heads + h;
-    const float l = part_ml[2 * r + 1];
-    const float w = (l > 0.0f) ? exp2f(part_ml[2 * r] - big_m) : 0.0f;
-    weight[s] = w;  // splits <= kMaxSplitWeights is checked on the host
-    lsum += w * l;
-  }
-  lsum = wave_sum(lsum);
-  __syncthreads();
-  if (tid % kWave == 0) red[tid / kWave] = lsum;
-  __syncthreads();
-  if (tid == 0) {
-    float l = 0.0f;
-    for (int w = 0; w < kMergeThreads / kWave; ++w) l += red[w];
-    bcast[1] = l;
-  }
-  __syncthreads();
-  const float big_l = bcast[1];
-
-  // 3) weighted sum of the unnormalised outputs of this 32-dim slice
-  const int dd = tid % kSliceDims;
-  const int ph = tid / kSliceDims;
-  float acc = 0.0f;
-  if (d0 + dd < head_dim) {
-    for (int s = ph; s < splits; s += kPhases) {
-      const float w = weight[s];
-      if (w != 0.0f) acc += w * part_o[(static_cast<long>(s) * query_heads + h) * head_dim + d0 + dd];
-    }
-  }
-  partial[ph][dd] = acc;
-  __syncthreads();
-  if (tid < kSliceDims && d0 + tid < head_dim) {
-    float sum = 0.0f;
+  const int dd = threadIdx.x % kSliceDims;
+  const int ph = threadIdx.x / kSliceDims;
+  const bool live = d0 + dd < head_dim;
+  const int dcol = live ? d0 + dd : d0;
+  float m = -INFINITY, l = 0.0f, o = 0.0f;
+  int s = ph;
+  for (; s + (kBatch - 1) * kPhases < splits; s += kBatch * kPhases) {
+    float ms[kBatch], ls[kBatch], os[kBatch];
 #pragma unroll
-    for (int q = 0; q < kPhases; ++q) sum += partial[q][tid];
-    out[static_cast<long>(h) * head_dim + d0 + tid] = big_l > 0.0f ? sum / big_l : 0.0f;
+    for (int b = 0; b < kBatch; ++b) {
+      const long r = static_cast<long>(s + b * kPhases) * query_heads + h;
+      ms[b] = part_ml[2 * r];
+      ls[b] = part_ml[2 * r + 1];
+      os[b] = part_o[r * head_dim + dcol];
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) fold(m, l, o, ms[b], ls[b], os[b]);
   }
-  if (tid == 0 && blockIdx.y == 0) lse[h] = big_l > 0.0f ? kLn2 * (big_m + log2f(big_l)) : -INFINITY;
+  for (; s < splits; s += kPhases) {
+    const long r = static_cast<long>(s) * query_heads + h;
+    fold(m, l, o, part_ml[2 * r], part_ml[2 * r + 1], part_o[r * head_dim + dcol]);
+  }
+  sm[ph][dd] = m;
+  sl[ph][dd] = l;
+  so[ph][dd] = o;
+  __syncthreads();
+  if (ph == 0) {
+#pragma unroll
+    for (int q = 1; q < kPhases; ++q) fold(m, l, o, sm[q][dd], sl[q][dd], so[q][dd]);
+    if (live) out[static_cast<long>(h) * head_dim + d0 + dd] = l > 0.0f ? o / l : 0.0f;
+    if (dd == 0 && blockIdx.y == 0) lse[h] = l > 0.0f ? kLn2 * (m + log2f(l)) : -INFINITY;
+  }
 }
 
 __global__ __launch_bounds__(kMergeThreads) void merge_chunks_kernel(int dim, float* __restrict__ acc_out,
@@ -128,7 +111,6 @@ __global__ __launch_bounds__(kMergeThreads) void merge_chunks_kernel(int dim, fl
 
 int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, float* out, float* lse,
                         hipStream_t stream) {
-  if (splits > kMaxSplitWeights) return arg_error("too many splits for the merge kernel");
   const int slices = (head_dim + kSliceDims - 1) / kSliceDims;
   hipLaunchKernelGGL(merge_splits_kernel, dim3(query_heads, slices), dim3(kMergeThreads), 0, stream, parts.o,
                      parts.ml, splits, query_heads, head_dim, out, lse);

@@ -64,11 +64,10 @@ def check(out, lse, ref_out, ref_lse, atol=ATOL, rtol=RTOL):
 
 
 def kernels_for(query, batch):
-    """Every kernel that supports this shape ("general" always, "mfma" when it applies)."""
-    names = ["general"]
-    if HipAttentionBackend("auto").kernel_for(query, batch) == "mfma":
-        names.append("mfma")
-    return names
+    """Every kernel that supports this shape: "general" always, then "mfma" and
+    "staged" when they apply (AUTO names the fastest)."""
+    best = HipAttentionBackend("auto").kernel_for(query, batch)
+    return {"general": ["general"], "mfma": ["general", "mfma"], "staged": ["general", "mfma", "staged"]}[best]
 
 
 # ------------------------------------------------------------------ codec ---
@@ -117,6 +116,10 @@ MATRIX = [
     (32, 8, 128, 32, 128),
     (64, 8, 128, 32, 128),
     (32, 8, 128, 32, 256),
+    (16, 4, 128, 32, 128),
+    (8, 8, 128, 32, 128),
+    (24, 12, 128, 32, 128),
+    (40, 8, 128, 32, 128),
 ]
 
 
@@ -227,7 +230,7 @@ def test_config_cpu_runnable_4096_tokens(cuda_device):
     scale = 1 / math.sqrt(128)
     ref_out, ref_lse = O.attention(q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, scale)
     query, batch = to_device(cuda_device, q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, torch.float16)
-    assert kernels_for(query, batch) == ["general", "mfma"]
+    assert kernels_for(query, batch) == ["general", "mfma", "staged"]
     for kernel in kernels_for(query, batch):
         out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
         check(out, lse, ref_out, ref_lse)
@@ -271,5 +274,21 @@ def test_misaligned_buffers_use_general_kernel(cuda_device):
     out, lse = auto.run(query, moved, 0.1)
     assert auto.last_kernel == "general"
     check(out, lse, ref_out, ref_lse)
-    with pytest.raises(ValueError, match="aligned"):
-        HipAttentionBackend("mfma").run(query, moved, 0.1)
+    for kernel in ("mfma", "staged"):
+        with pytest.raises(ValueError, match="aligned"):
+            HipAttentionBackend(kernel).run(query, moved, 0.1)
+
+
+def test_int2_8_byte_aligned_buffers_use_mfma_kernel(cuda_device):
+    # 8-byte aligned INT2 rows suit the register-staged kernel, not the 16-byte copies
+    q, pk, pv, sk, sv, valid = make_batch(6, 32, 8, 128, 2, 128, 2, 32)
+    ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, 2, 32, 0.1)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, 2, 32)
+    raw = torch.empty(batch.packed_v.numel() + 8, dtype=torch.uint8, device=cuda_device)
+    shifted = raw[8:].view(batch.packed_v.shape)
+    shifted.copy_(batch.packed_v)
+    moved = PackedBatch(batch.packed_k, shifted, batch.scales_k, batch.scales_v, batch.valid_tokens, 2, 32)
+    auto = HipAttentionBackend("auto")
+    out, lse = auto.run(query, moved, 0.1)
+    assert auto.last_kernel == "mfma"
+    check(out, lse, ref_out, ref_lse)

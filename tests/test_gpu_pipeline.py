@@ -98,8 +98,8 @@ def test_full_size_128k_tokens(cuda_device, bits, value_scale, outliers):
     dev = cuda_device
     query = q.to(dev)
     batch = PackedBatch(*(torch.from_numpy(a).to(dev) for a in (pk, pv, sk, sv, valid)), bits, 32)
-    for kernel in ["general", "mfma"]:
-        backend = HipAttentionBackend(kernel if kernel == "general" else "auto")
+    for kernel in ["general", "mfma", "staged"]:
+        backend = HipAttentionBackend(kernel)
         out, lse = backend.run(query, batch, scale)
         np.testing.assert_allclose(out.cpu().numpy(), ref_out, atol=ATOL, rtol=RTOL)
         np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=ATOL, rtol=RTOL)
@@ -121,7 +121,7 @@ def test_sparse_selection_262k_tokens(cuda_device):
     ref_out, ref_lse = O.attention(q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, scale, block_table=table)
     dev = cuda_device
     batch = PackedBatch(*(torch.from_numpy(a).to(dev) for a in (pk, pv, sk, sv, valid)), 4, 32)
-    for kernel in ["general", "auto"]:
+    for kernel in ["general", "mfma", "staged"]:
         out, lse = HipAttentionBackend(kernel).run(q.to(dev), batch, scale, block_table=ids)
         np.testing.assert_allclose(out.cpu().numpy(), ref_out, atol=ATOL, rtol=RTOL)
         np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=ATOL, rtol=RTOL)
