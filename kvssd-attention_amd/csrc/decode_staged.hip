@@ -60,7 +60,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void lds_void_t;
 
 constexpr int kKG = 4;               // kv heads per workgroup
 constexpr int kWaves = 2 * kKG;      // (kv head, token half)
@@ -136,42 +135,26 @@ __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)p));
 }
 
-// ds_read_b64_tr_b4 pairs (offsets 0 and 8 of each address): within each group
-// of 16 lanes, lane j receives nibble j of the 8 bytes every lane of the group
-// addressed, lane r's nibble landing in bits 4r..4r+3 (a 16x16 nibble
-// transpose).  Issued from asm, with its own lgkmcnt wait before the results
-// are handed back: the compiler's intrinsic form of this read carries no
-// memory operand, so the compiler would make it wait for every outstanding
-// global->LDS copy, i.e. for the next stage's prefetch.
-__device__ __forceinline__ void tr4_pairs4(uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3, i32x2 (&r)[8]) {
-  asm volatile(
-      "ds_read_b64_tr_b4 %0, %8\n\t"
-      "ds_read_b64_tr_b4 %1, %8 offset:8\n\t"
-      "ds_read_b64_tr_b4 %2, %9\n\t"
-      "ds_read_b64_tr_b4 %3, %9 offset:8\n\t"
-      "ds_read_b64_tr_b4 %4, %10\n\t"
-      "ds_read_b64_tr_b4 %5, %10 offset:8\n\t"
-      "ds_read_b64_tr_b4 %6, %11\n\t"
-      "ds_read_b64_tr_b4 %7, %11 offset:8\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]), "=&v"(r[6]), "=&v"(r[7])
-      : "v"(a0), "v"(a1), "v"(a2), "v"(a3)
-      : "memory");
-}
-__device__ __forceinline__ void tr4_pairs2(uint32_t a0, uint32_t a1, i32x2 (&r)[4]) {
-  asm volatile(
-      "ds_read_b64_tr_b4 %0, %4\n\t"
-      "ds_read_b64_tr_b4 %1, %4 offset:8\n\t"
-      "ds_read_b64_tr_b4 %2, %5\n\t"
-      "ds_read_b64_tr_b4 %3, %5 offset:8\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
-      : "v"(a0), "v"(a1)
-      : "memory");
+// ds_read_b64_tr_b4: within each group of 16 lanes, lane j receives nibble j of
+// the 8 bytes every lane of the group addressed, lane r's nibble landing in
+// bits 4r..4r+3 (a 16x16 nibble transpose).
+__device__ __forceinline__ i32x2 lds_read_tr4(const uint8_t* lds, int offset) {
+  typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+  return __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2*)(lds + offset));
 }
 
-__device__ __forceinline__ void dma16(const uint8_t* src, uint8_t* lds_dst) {
-  __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (lds_void_t*)(lds_dst), 16, 0, 0);
+// One global -> LDS copy instruction: lane i's 16 bytes from sbase + voff land
+// at LDS byte lds_dst + 16 i.  Issued from asm so that the compiler does not
+// treat it as a pending write to every LDS location: in its intrinsic form the
+// compiler waits for all outstanding copies (i.e. the next stage's prefetch)
+// before any LDS read it cannot tell apart from them.  The copies' completion
+// is awaited explicitly (vmcnt) before the barrier that publishes a stage.
+// M0 is a reserved register the compiler does not track through asm clobbers;
+// this kernel has no other M0 user (no compiler-issued LDS copies, dynamic
+// register indexing or messages), so the asm owns it.
+__device__ __forceinline__ void dma16(const uint8_t* sbase, uint32_t voff, uint32_t lds_dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_dst)
+               : "memory");
 }
 
 // ---------------------------------------------------------- code -> fp16 ---
@@ -299,7 +282,7 @@ __device__ __forceinline__ CopyMap<BITS> make_copy_map(int wave, int lane, int k
 }
 
 template <int BITS>
-__device__ __forceinline__ void issue_stage(const StagedParams& p, uint8_t* buf, const Cursor& c, int kvh0, int wave,
+__device__ __forceinline__ void issue_stage(const StagedParams& p, uint32_t buf, const Cursor& c, int kvh0, int wave,
                                             const CopyMap<BITS>& cm) {
   using G = Geo<BITS>;
   const long row0 = (static_cast<long>(c.blk) * p.block_tokens + c.sb0) * p.kv_heads + kvh0;
@@ -307,12 +290,12 @@ __device__ __forceinline__ void issue_stage(const StagedParams& p, uint8_t* buf,
   const uint8_t* vb = p.pv + row0 * G::PD;
 #pragma unroll
   for (int j = 0; j < G::KV_PER_WAVE; ++j) {
-    const int i = wave + kWaves * j;
-    dma16(kb + cm.kv[j], buf + G::K_OFF + 1024 * i);
-    dma16(vb + cm.kv[j], buf + G::V_OFF + 1024 * i);
+    const uint32_t i = static_cast<uint32_t>(wave + kWaves * j);
+    dma16(kb, cm.kv[j], buf + G::K_OFF + 1024u * i);
+    dma16(vb, cm.kv[j], buf + G::V_OFF + 1024u * i);
   }
   const uint8_t* sb = (wave < 4 ? p.sk : p.sv) + row0 * 8;
-  dma16(sb + cm.sc, buf + (wave < 4 ? G::SK_OFF : G::SV_OFF) + 1024 * (wave & 3));
+  dma16(sb, cm.sc, buf + (wave < 4 ? G::SK_OFF : G::SV_OFF) + 1024u * static_cast<uint32_t>(wave & 3));
 }
 
 // W chunk (quad, row R = 4h + g, chunk c of 8 slots) byte offset.
@@ -395,46 +378,117 @@ struct WaveState {
 };
 
 // One stage of one wave: tokens 64*half .. 64*half + hv - 1 of the stage are valid.
+// Every LDS read of the stage goes out first, the four tiles' QK chains are
+// interleaved and V is unpacked before the softmax, so the two waves of a
+// SIMD have independent work to fill each other's latencies.
 template <int BITS, int QUADS, int QSPLIT>
 __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase, int hv, int w, int half, int li,
                                               int lq, const Masks& mk, const QueryOps<QUADS, QSPLIT>& qo,
                                               const u32x4 (&offa)[BITS == 4 ? 1 : 2], WaveState<BITS, QUADS>& st) {
   using G = Geo<BITS>;
-  // ---------------------------------------------------------------- QK
-  float score[QUADS][4];
-  u32x2 svw[4];
+  constexpr int KW = BITS == 4 ? 4 : 2;   // K words per lane and tile
+  constexpr int NTR = BITS == 4 ? 8 : 4;  // transpose reads (16 / 32 dims each)
+  constexpr int NPAR = BITS == 4 ? 1 : 2;
+  // ------------------------------------------------------------ LDS reads
+  uint32_t kraw[4][KW];
+  u32x2 skw[4], svw[4];
 #pragma unroll
   for (int tau = 0; tau < 4; ++tau) {
     const int t = kHalfTok * half + 16 * tau + li;
-    u32x4 b[4];
     if (BITS == 4) {
-      const u32x4 raw = *reinterpret_cast<const u32x4*>(buf + G::K_OFF + chunk_byte<16>(t, 4 * w + lq));
+      const u32x4 r = *reinterpret_cast<const u32x4*>(buf + G::K_OFF + chunk_byte<16>(t, 4 * w + lq));
 #pragma unroll
-      for (int m = 0; m < 4; ++m) b[m] = unpack4(raw[m], mk);
+      for (int i = 0; i < KW; ++i) kraw[tau][i] = r[i];
     } else {
-      const u32x2 raw =
+      const u32x2 r =
           *reinterpret_cast<const u32x2*>(buf + G::K_OFF + chunk_byte<8>(t, 2 * w + (lq >> 1)) + 8 * (lq & 1));
 #pragma unroll
-      for (int m = 0; m < 4; ++m) b[m] = unpack2(raw[m >> 1], m & 1, mk);
+      for (int i = 0; i < KW; ++i) kraw[tau][i] = r[i];
     }
     const int sbyte = chunk_byte<2>(t, w >> 1) + 8 * (w & 1);
-    const u32x2 skw = *reinterpret_cast<const u32x2*>(buf + G::SK_OFF + sbyte);
+    skw[tau] = *reinterpret_cast<const u32x2*>(buf + G::SK_OFF + sbyte);
     svw[tau] = *reinterpret_cast<const u32x2*>(buf + G::SV_OFF + sbyte);
-    const bool ok = 16 * tau + li < hv;
+  }
+  // transpose-read row of this lane: kk = li >> 3, row rho = li & 7,
+  // slot s = 2(rho & 3) + (rho >> 2) -> token 16(s&3) + 4lq + 2kk + (s>>2)
+  const int rho = li & 7;
+  const int s_tr = ((rho & 3) << 1) | (rho >> 2);
+  const int t_tr = kHalfTok * half + 16 * (s_tr & 3) + 4 * lq + 2 * (li >> 3) + (s_tr >> 2);
+  // (two query quads keep twice the accumulators live: their V reads and
+  // unpack wait until after the softmax so the operands fit the registers)
+  constexpr bool kEarlyV = QUADS == 1;
+  i32x2 tr[NTR];
+  auto read_v = [&]() {
 #pragma unroll
-    for (int quad = 0; quad < QUADS; ++quad) {
-      f32x4 cc = qo.qcorr[quad];
+    for (int n = 0; n < NTR; ++n)
+      tr[n] = BITS == 4 ? lds_read_tr4(buf, G::V_OFF + chunk_byte<16>(t_tr, 4 * w + (n >> 1)) + 8 * (n & 1))
+                        : lds_read_tr4(buf, G::V_OFF + chunk_byte<8>(t_tr, 2 * w + (n >> 1)) + 8 * (n & 1));
+  };
+  if constexpr (kEarlyV) read_v();
+  // ---------------------------------------------------------------- QK
+  f32x4 cc[QUADS][4];
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad)
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau) cc[quad][tau] = qo.qcorr[quad];
+  if constexpr (kEarlyV) {
+    // the four tiles' chains interleaved, one K word position at a time
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      u32x4 b[4];
+#pragma unroll
+      for (int tau = 0; tau < 4; ++tau)
+        b[tau] = BITS == 4 ? unpack4(kraw[tau][m], mk) : unpack2(kraw[tau][m >> 1], m & 1, mk);
 #pragma unroll
       for (int sp = 0; sp < QSPLIT; ++sp)
 #pragma unroll
-        for (int m = 0; m < 4; ++m) cc = mfma16(qo.qa[quad][sp][m], b[m], cc);
-      float raw = __builtin_fmaf(half_lo(skw[0]), cc[0], 0.0f);
-      raw = __builtin_fmaf(half_hi(skw[0]), cc[1], raw);
-      raw = __builtin_fmaf(half_lo(skw[1]), cc[2], raw);
-      raw = __builtin_fmaf(half_hi(skw[1]), cc[3], raw);
+        for (int quad = 0; quad < QUADS; ++quad)
+#pragma unroll
+          for (int tau = 0; tau < 4; ++tau) cc[quad][tau] = mfma16(qo.qa[quad][sp][m], b[tau], cc[quad][tau]);
+    }
+  } else {
+    // tile by tile (fewer live operands)
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau) {
+      u32x4 b[4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        b[m] = BITS == 4 ? unpack4(kraw[tau][m], mk) : unpack2(kraw[tau][m >> 1], m & 1, mk);
+#pragma unroll
+      for (int quad = 0; quad < QUADS; ++quad)
+#pragma unroll
+        for (int sp = 0; sp < QSPLIT; ++sp)
+#pragma unroll
+          for (int m = 0; m < 4; ++m) cc[quad][tau] = mfma16(qo.qa[quad][sp][m], b[m], cc[quad][tau]);
+    }
+  }
+  float score[QUADS][4];
+#pragma unroll
+  for (int tau = 0; tau < 4; ++tau) {
+    const bool ok = 16 * tau + li < hv;
+#pragma unroll
+    for (int quad = 0; quad < QUADS; ++quad) {
+      const f32x4 c = cc[quad][tau];
+      float raw = __builtin_fmaf(half_lo(skw[tau][0]), c[0], 0.0f);
+      raw = __builtin_fmaf(half_hi(skw[tau][0]), c[1], raw);
+      raw = __builtin_fmaf(half_lo(skw[tau][1]), c[2], raw);
+      raw = __builtin_fmaf(half_hi(skw[tau][1]), c[3], raw);
       score[quad][tau] = ok ? raw * qo.kscale[quad] : -INFINITY;
     }
   }
+  // --------------------------------------------- V operands (no softmax dep)
+  u32x4 va[NTR][2][NPAR];
+  auto unpack_v = [&]() {
+#pragma unroll
+    for (int n = 0; n < NTR; ++n)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int par = 0; par < NPAR; ++par)
+          va[n][kk][par] = BITS == 4 ? unpack4(static_cast<uint32_t>(tr[n][kk]), mk)
+                                     : unpack2_tr(static_cast<uint32_t>(tr[n][kk]), par, mk);
+  };
+  if constexpr (kEarlyV) unpack_v();
   // unit of this lane's W slots (4 tiles) in its (h, g) rows
   const int u = 8 * ((li >> 1) & 1) + 2 * (li >> 2) + (li & 1);
   // --------------------------------------------------------------- softmax
@@ -480,60 +534,36 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
 #pragma unroll
       for (int n = 0; n < 8; ++n) st.acc[quad][n] *= a_pv;
 #pragma unroll
-      for (int c = 0; c < (BITS == 4 ? 1 : 2); ++c) st.corr[quad][c] *= a_pv;
+      for (int c = 0; c < NPAR; ++c) st.corr[quad][c] *= a_pv;
     }
   }
   // -------------------------------------------------------------------- PV
+  if constexpr (!kEarlyV) {
+    read_v();
+    unpack_v();
+  }
   u32x4 wb[QUADS][2];
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
       wb[quad][kk] = *reinterpret_cast<const u32x4*>(wbase + w_chunk<BITS, QUADS>(quad, li, 4 * kk + lq, w, half));
-  // transpose-read row of this lane: kk = li >> 3, row rho = li & 7,
-  // slot s = 2(rho & 3) + (rho >> 2) -> token 16(s&3) + 4lq + 2kk + (s>>2)
-  const int rho = li & 7;
-  const int s_tr = ((rho & 3) << 1) | (rho >> 2);
-  const int t_tr = kHalfTok * half + 16 * (s_tr & 3) + 4 * lq + 2 * (li >> 3) + (s_tr >> 2);
-  const uint32_t vbase = lds_addr(buf + G::V_OFF);
-  if (BITS == 4) {
-    i32x2 trs[8];
-    tr4_pairs4(vbase + chunk_byte<16>(t_tr, 4 * w), vbase + chunk_byte<16>(t_tr, 4 * w + 1),
-               vbase + chunk_byte<16>(t_tr, 4 * w + 2), vbase + chunk_byte<16>(t_tr, 4 * w + 3), trs);
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
-      const i32x2 tr = trs[n];
+  for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const u32x4 a = unpack4(static_cast<uint32_t>(tr[kk]), mk);
+    for (int n = 0; n < NTR; ++n)
 #pragma unroll
-        for (int quad = 0; quad < QUADS; ++quad) st.acc[quad][n] = mfma16(a, wb[quad][kk], st.acc[quad][n]);
-      }
-    }
-  } else {
-    i32x2 trs[4];
-    tr4_pairs2(vbase + chunk_byte<8>(t_tr, 2 * w), vbase + chunk_byte<8>(t_tr, 2 * w + 1), trs);
+      for (int par = 0; par < NPAR; ++par)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      const i32x2 tr = trs[n];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-        for (int par = 0; par < 2; ++par) {
-          const u32x4 a = unpack2_tr(static_cast<uint32_t>(tr[kk]), par, mk);
-#pragma unroll
-          for (int quad = 0; quad < QUADS; ++quad)
-            st.acc[quad][2 * n + par] = mfma16(a, wb[quad][kk], st.acc[quad][2 * n + par]);
-        }
-    }
-  }
+        for (int quad = 0; quad < QUADS; ++quad)
+          st.acc[quad][NPAR * n + par] = mfma16(va[n][kk][par], wb[quad][kk], st.acc[quad][NPAR * n + par]);
   // sum over tokens of W * OFF per column, through the matrix core
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int c = 0; c < (BITS == 4 ? 1 : 2); ++c) st.corr[quad][c] = mfma16(offa[c], wb[quad][kk], st.corr[quad][c]);
+      for (int c = 0; c < NPAR; ++c) st.corr[quad][c] = mfma16(offa[c], wb[quad][kk], st.corr[quad][c]);
 }
 
 template <int BITS, int QUADS, int QSPLIT, typename QT>
@@ -549,15 +579,34 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   const int li = lane & 15;
   const int lq = lane >> 4;
 
-  // workgroup -> (split, group of 4 kv heads); the two groups of a split read
-  // the two halves of the same token rows at about the same time
+  // workgroup -> (split, group of 4 kv heads).  Consecutive workgroup ids go
+  // to different XCDs (round robin over 8); every group of split s gets an id
+  // with id % 8 == s % 8, so they share one XCD and its L2: the groups read
+  // complementary parts of the same 128-byte lines of the scale rows.
   const int groups = p.kv_heads / kKG;
-  const int grp = blockIdx.x % groups;
-  const int split = blockIdx.x / groups;
+  const int xcd = blockIdx.x & 7;
+  const int rest = blockIdx.x >> 3;
+  const int grp = rest % groups;
+  const int split = (rest / groups) * 8 + xcd;
+  if (split >= p.splits) return;  // padding ids of the last round
   const int u_begin = split * p.blocks_per_split;
   const int u_end = min(p.units, u_begin + p.blocks_per_split);
   const int kvh0 = grp * kKG;
   const int head0 = (kvh0 + w) * p.gq;
+
+  // The first stage's copies go out before anything else: the split's first
+  // attended block, tokens 0..127 (one scalar read with a block table).  If
+  // that block holds no valid token they are simply not used.
+  const CopyMap<BITS> cm = make_copy_map<BITS>(wave, lane, p.kv_heads);
+  const uint32_t lds0 = lds_addr(lds);
+  bool spec = false;
+  if (u_begin < u_end) {
+    Cursor c0{0, __builtin_amdgcn_readfirstlane(p.table ? p.table[u_begin] : u_begin), 0, 0};
+    if (c0.blk >= 0 && c0.blk < p.num_blocks) {
+      issue_stage<BITS>(p, lds0, c0, kvh0, wave, cm);
+      spec = true;
+    }
+  }
 
   // the split's (block id, clamped valid count) list, read once into LDS
   int* units = reinterpret_cast<int*>(lds + 2 * G::STAGE + kWBytes);
@@ -569,10 +618,14 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   }
   __syncthreads();
 
-  const CopyMap<BITS> cm = make_copy_map<BITS>(wave, lane, p.kv_heads);
   Cursor cur{-1, 0, 0, -kStageTok};
   bool have = next_stage(cur, units, n_units);
-  if (have) issue_stage<BITS>(p, lds, cur, kvh0, wave, cm);
+  if (have && !(spec && cur.u == 0 && cur.sb0 == 0)) {
+    // the first valid stage is elsewhere: let this wave's early copies land
+    // (they target the same LDS chunks), then load the right ones
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    issue_stage<BITS>(p, lds0, cur, kvh0, wave, cm);
+  }
 
   QueryOps<QUADS, QSPLIT> qo;
   setup_query<BITS, QUADS, QSPLIT, QT>(qo, p, head0, li, lq);
@@ -598,19 +651,24 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   }
 
   // ------------------------------------------- double-buffered stage loop
+  // the stage after the current one is looked up a step ahead, so that its
+  // copies go out right after the barrier
+  Cursor nxt = cur;
+  bool have_n = have && next_stage(nxt, units, n_units);
   int buf = 0;
   while (have) {
-    const Cursor c0 = cur;
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
     __syncthreads();                     // ... everyone's; and the other buffer is free
-    have = next_stage(cur, units, n_units);
-    if (have) issue_stage<BITS>(p, lds + (buf ^ 1) * G::STAGE, cur, kvh0, wave, cm);
-    const int hv = min(kStageTok, c0.vb - c0.sb0) - kHalfTok * half;
+    if (have_n) issue_stage<BITS>(p, lds0 + static_cast<uint32_t>((buf ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
+    const int hv = min(kStageTok, cur.vb - cur.sb0) - kHalfTok * half;
     if (hv > 0) {
       uint8_t* sbuf = lds + buf * G::STAGE;
       uint8_t* wbase = G::W_IN_K ? sbuf : lds + 2 * G::STAGE + wave * QUADS * 2048;
       compute_stage<BITS, QUADS, QSPLIT>(sbuf, wbase, hv, w, half, li, lq, mk, qo, offa, st);
     }
+    cur = nxt;
+    have = have_n;
+    if (have) have_n = next_stage(nxt, units, n_units);
     buf ^= 1;
   }
 
@@ -619,7 +677,8 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // lane (li, lq): column (head li/4, group li%4), rows = dims of its tiles
   float* xo = reinterpret_cast<float*>(lds);  // [w][quad][lane][8] from half 1
   float* xm = xo + kKG * QUADS * 64 * 8;      // [w][quad][4 heads][2]
-  __syncthreads();  // every wave is done with the stage buffers
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // no copy of this wave is still writing LDS
+  __syncthreads();                     // every wave is done with the stage buffers
   float ov[QUADS][8];
   float mh[QUADS], lh[QUADS];
 #pragma unroll
@@ -772,7 +831,7 @@ int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials part
   prm.blocks_per_split = plan.blocks_per_split;
   prm.gq = d.query_heads / d.kv_heads;
   prm.scale_log2 = static_cast<float>(d.sm_scale) * kLog2e;
-  const int grid = plan.splits * (d.kv_heads / kKG);
+  const int grid = 8 * (d.kv_heads / kKG) * ((plan.splits + 7) / 8);
   const bool two = prm.gq > 4;
   if (d.bits == 4) return two ? launch_quads<4, 2>(prm, grid, d.query_dtype, a.stream)
                               : launch_quads<4, 1>(prm, grid, d.query_dtype, a.stream);
