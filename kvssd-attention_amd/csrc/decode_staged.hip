@@ -166,8 +166,8 @@ __device__ __forceinline__ void dma16(const uint8_t* sbase, uint32_t voff, uint3
 // result needs.  (Codes left in place as fp16 subnormals would save shifts,
 // but the matrix core does not multiply subnormal operands exactly against
 // operands of wide exponent range.)  One shift per distinct distance plus one
-// AND-OR per fp16 pair; the masks live in VGPRs so the backend can fuse AND +
-// OR into v_and_or_b32 (it may read only one scalar operand).
+// AND-OR per fp16 pair; the masks live in VGPRs (a three-operand VALU op may
+// read only one scalar).
 struct Masks {
   uint32_t m47;  // bits 4-7 of both halves (INT4, F = 64)
   uint32_t m89;  // bits 8-9 (INT2, F = 4)
@@ -178,7 +178,9 @@ __device__ __forceinline__ Masks make_masks(uint32_t opaque_zero) {
   return Masks{0x00F000F0u | opaque_zero, 0x03000300u | opaque_zero, 0x00C000C0u | opaque_zero};
 }
 
-__device__ __forceinline__ uint32_t ao(uint32_t x, uint32_t m) { return (x & m) | kF16One2; }
+// (x & m) | 1.0-pairs as one v_bitop3_b32 (truth table 0xEA = (a & b) | c): a
+// compiler builtin, so the hazard recognizer sees it like any VALU op.
+__device__ __forceinline__ uint32_t ao(uint32_t x, uint32_t m) { return __builtin_amdgcn_bitop3_b32(x, m, kF16One2, 0xEA); }
 
 // INT4 word x (nibbles n0..n7, n_i at bits 4i): fp16 slots s0..s7 hold
 // n0, n4, n1, n5, n2, n6, n3, n7 (slot s <-> nibble (s>>1) + 4(s&1)), F = 64.

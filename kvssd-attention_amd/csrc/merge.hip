@@ -4,8 +4,7 @@
 // (O_s unnormalised, m_s in log2 units, l_s = sum 2^(s - m_s)):
 //   M = max_s m_s,  L = sum_s l_s 2^(m_s - M),
 //   out = sum_s O_s 2^(m_s - M) / L,  lse = ln 2 * (M + log2 L),
-// evaluated as a running fold (m, l, o) <- (max, rescaled sums), which gives
-// the same M and the same terms.
+// with the weights 2^(m_s - M) formed once per (head, split).
 // Splits with l_s = 0 (no valid token) contribute nothing; if every split is
 // empty, out = 0 and lse = -inf (attention over an empty token set, as
 // src/kvssd/backends/reference.py:46-49 returns it).
@@ -19,65 +18,91 @@ namespace kvssd {
 namespace {
 
 constexpr int kMergeThreads = 256;
+constexpr int kMaxMergeSplits = 2048;
 
-// One workgroup per (query head, 32-dim slice); thread (phase, dim) folds the
-// splits s = phase (mod 8) into a running (m, l, o) with the online rescaling
-// (loads 16 splits at a time so their latencies overlap), then the 8 phases
-// meet in LDS.  One pass over the partials, no second round trip for the
-// global max.
+// One workgroup per (query head, 32-dim slice); thread (phase, dim) owns the
+// splits s = phase (mod 8) of one dim.  Its first 16 O loads go out together
+// with the workgroup's load of every split's (m, l), so the common case
+// (<= 128 splits) costs one round trip to memory; the split weights
+// 2^(m_s - M) are formed once, in LDS, and the 8 phases meet in LDS at the end.
 constexpr int kSliceDims = 32;
 constexpr int kPhases = kMergeThreads / kSliceDims;  // 8
 constexpr int kBatch = 16;
-
-__device__ __forceinline__ void fold(float& m, float& l, float& o, float ms, float ls, float os) {
-  if (ls > 0.0f) {
-    const float mn = fmaxf(m, ms);
-    const float a = exp2f(m - mn);  // m = -inf on the first fold: a = 0
-    const float b = exp2f(ms - mn);
-    o = o * a + os * b;
-    l = l * a + ls * b;
-    m = mn;
-  }
-}
 
 __global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(const float* __restrict__ part_o,
                                                                      const float* __restrict__ part_ml, int splits,
                                                                      int query_heads, int head_dim,
                                                                      float* __restrict__ out, float* __restrict__ lse) {
-  __shared__ float sm[kPhases][kSliceDims], sl[kPhases][kSliceDims], so[kPhases][kSliceDims];
+  __shared__ float sw[kMaxMergeSplits];  // m_s, then the weight 2^(m_s - M) (0 for empty splits)
+  __shared__ float sl[kMaxMergeSplits];
+  __shared__ float red[kMergeThreads / kWave];
+  __shared__ float partial[kPhases][kSliceDims];
   const int h = blockIdx.x;
   const int d0 = blockIdx.y * kSliceDims;
-  const int dd = threadIdx.x % kSliceDims;
-  const int ph = threadIdx.x / kSliceDims;
+  const int tid = threadIdx.x;
+  const int dd = tid % kSliceDims;
+  const int ph = tid / kSliceDims;
   const bool live = d0 + dd < head_dim;
   const int dcol = live ? d0 + dd : d0;
-  float m = -INFINITY, l = 0.0f, o = 0.0f;
-  int s = ph;
-  for (; s + (kBatch - 1) * kPhases < splits; s += kBatch * kPhases) {
-    float ms[kBatch], ls[kBatch], os[kBatch];
+
+  float ov[kBatch];
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const long r = static_cast<long>(s + b * kPhases) * query_heads + h;
-      ms[b] = part_ml[2 * r];
-      ls[b] = part_ml[2 * r + 1];
-      os[b] = part_o[r * head_dim + dcol];
-    }
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) fold(m, l, o, ms[b], ls[b], os[b]);
+  for (int j = 0; j < kBatch; ++j) {
+    const int s = ph + kPhases * j;
+    ov[j] = s < splits ? part_o[(static_cast<long>(s) * query_heads + h) * head_dim + dcol] : 0.0f;
   }
-  for (; s < splits; s += kPhases) {
+  float mx = -INFINITY;
+  for (int s = tid; s < splits; s += kMergeThreads) {
     const long r = static_cast<long>(s) * query_heads + h;
-    fold(m, l, o, part_ml[2 * r], part_ml[2 * r + 1], part_o[r * head_dim + dcol]);
+    const float m = part_ml[2 * r], l = part_ml[2 * r + 1];
+    sw[s] = m;
+    sl[s] = l;
+    if (l > 0.0f) mx = fmaxf(mx, m);
   }
-  sm[ph][dd] = m;
-  sl[ph][dd] = l;
-  so[ph][dd] = o;
+  // M = max over non-empty splits
+  mx = wave_max(mx);
+  if (tid % kWave == 0) red[tid / kWave] = mx;
+  __syncthreads();
+  float big_m = red[0];
+#pragma unroll
+  for (int w = 1; w < kMergeThreads / kWave; ++w) big_m = fmaxf(big_m, red[w]);
+  // weights and L = sum_s w_s l_s
+  float lsum = 0.0f;
+  for (int s = tid; s < splits; s += kMergeThreads) {
+    const float l = sl[s];
+    const float w = l > 0.0f ? exp2f(sw[s] - big_m) : 0.0f;
+    sw[s] = w;
+    lsum += w * l;
+  }
+  lsum = wave_sum(lsum);
+  __syncthreads();  // every lane has read red[] before it is reused
+  if (tid % kWave == 0) red[tid / kWave] = lsum;
+  __syncthreads();  // weights and partial sums visible
+  float big_l = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kMergeThreads / kWave; ++w) big_l += red[w];
+
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kBatch; ++j) {
+    const int s = ph + kPhases * j;
+    if (s < splits) {
+      const float w = sw[s];
+      if (w != 0.0f) acc += w * ov[j];
+    }
+  }
+  for (int s = ph + kPhases * kBatch; s < splits; s += kPhases) {
+    const float w = sw[s];
+    if (w != 0.0f) acc += w * part_o[(static_cast<long>(s) * query_heads + h) * head_dim + dcol];
+  }
+  partial[ph][dd] = acc;
   __syncthreads();
   if (ph == 0) {
+    float sum = 0.0f;
 #pragma unroll
-    for (int q = 1; q < kPhases; ++q) fold(m, l, o, sm[q][dd], sl[q][dd], so[q][dd]);
-    if (live) out[static_cast<long>(h) * head_dim + d0 + dd] = l > 0.0f ? o / l : 0.0f;
-    if (dd == 0 && blockIdx.y == 0) lse[h] = l > 0.0f ? kLn2 * (m + log2f(l)) : -INFINITY;
+    for (int q = 0; q < kPhases; ++q) sum += partial[q][dd];
+    if (live) out[static_cast<long>(h) * head_dim + d0 + dd] = big_l > 0.0f ? sum / big_l : 0.0f;
+    if (dd == 0 && blockIdx.y == 0) lse[h] = big_l > 0.0f ? kLn2 * (big_m + log2f(big_l)) : -INFINITY;
   }
 }
 
@@ -111,6 +136,7 @@ __global__ __launch_bounds__(kMergeThreads) void merge_chunks_kernel(int dim, fl
 
 int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, float* out, float* lse,
                         hipStream_t stream) {
+  if (splits > kMaxMergeSplits) return arg_error("too many splits for the merge kernel");
   const int slices = (head_dim + kSliceDims - 1) / kSliceDims;
   hipLaunchKernelGGL(merge_splits_kernel, dim3(query_heads, slices), dim3(kMergeThreads), 0, stream, parts.o,
                      parts.ml, splits, query_heads, head_dim, out, lse);
