@@ -139,7 +139,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="int4_gqa_128k", choices=sorted(WORKLOADS))
-    ap.add_argument("--kernel", default="auto", choices=["auto", "general", "mfma", "staged"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "general", "mfma", "staged", "pairs"])
     ap.add_argument("--copies", type=int, default=0, help="distinct KV copies rotated across steps (0 = auto)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument(
@@ -277,7 +277,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if kernel_name in ("mfma", "staged") else "f32",
+        "dtype": "f16" if kernel_name in ("mfma", "staged", "pairs") else "f32",
         "data": "synthetic",
         "config": {
             "workload": args.workload,

@@ -45,8 +45,11 @@ enum kvssd_kernel {
   KVSSD_KERNEL_AUTO = 0,    /* fastest kernel that supports the shape */
   KVSSD_KERNEL_GENERAL = 1, /* any shape the reference accepts */
   KVSSD_KERNEL_MFMA = 2,    /* matrix-core kernel: head_dim 128, group_size 32 */
-  KVSSD_KERNEL_STAGED = 3   /* LDS-staged matrix-core kernel: as MFMA, plus
+  KVSSD_KERNEL_STAGED = 3,  /* LDS-staged matrix-core kernel: as MFMA, plus
                                kv_heads % 4 == 0 and 16-byte aligned arrays */
+  KVSSD_KERNEL_PAIRS = 4    /* pair-owned LDS-staged matrix-core kernel: as
+                               STAGED, INT4 only, <= 4 query heads per kv head;
+                               used only when named (AUTO picks STAGED) */
 };
 
 /* Shape of one decode call.  The packed arrays follow the reference's

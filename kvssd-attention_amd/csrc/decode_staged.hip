@@ -50,16 +50,10 @@
 //   slot s -> token 16*(s&3) + 4q + 2kk + (s>>2) of the half; QK tile tau,
 //   lane li -> token 16*tau + li.  W of QK lane li, tile tau lives in slot
 //   4*u + tau of its (h, g) row, u = 8((li>>1)&1) + 2(li>>2) + (li&1).
-#include "decode.hpp"
+#include "staged_ops.hpp"
 
 namespace kvssd {
 namespace {
-
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kKG = 4;               // kv heads per workgroup
 constexpr int kWaves = 2 * kKG;      // (kv head, token half)
@@ -102,21 +96,6 @@ struct StagedParams {
   float scale_log2;  // sm_scale * log2(e)
 };
 
-// ------------------------------------------------------------ small helpers
-
-__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c, 0,
-                                                0, 0);
-}
-
-__device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
-  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
-         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
-}
-
-__device__ __forceinline__ float half_lo(uint32_t x) { return half_bits_to_float(static_cast<uint16_t>(x & 0xFFFFu)); }
-__device__ __forceinline__ float half_hi(uint32_t x) { return half_bits_to_float(static_cast<uint16_t>(x >> 16)); }
-
 // XOR swizzle of a region's chunk index for token t (CPT chunks per token).
 template <int CPT>
 __device__ __forceinline__ int phi(int t) {
@@ -128,144 +107,6 @@ __device__ __forceinline__ int phi(int t) {
 template <int CPT>
 __device__ __forceinline__ int chunk_byte(int t, int idx) {
   return 16 * (t * CPT + (idx ^ phi<CPT>(t)));
-}
-
-// LDS byte address of a pointer into a __shared__ array
-__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)p));
-}
-
-// ds_read_b64_tr_b4: within each group of 16 lanes, lane j receives nibble j of
-// the 8 bytes every lane of the group addressed, lane r's nibble landing in
-// bits 4r..4r+3 (a 16x16 nibble transpose).
-__device__ __forceinline__ i32x2 lds_read_tr4(const uint8_t* lds, int offset) {
-  typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
-  return __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2*)(lds + offset));
-}
-
-// One global -> LDS copy instruction: lane i's 16 bytes from sbase + voff land
-// at LDS byte lds_dst + 16 i.  Issued from asm so that the compiler does not
-// treat it as a pending write to every LDS location: in its intrinsic form the
-// compiler waits for all outstanding copies (i.e. the next stage's prefetch)
-// before any LDS read it cannot tell apart from them.  The copies' completion
-// is awaited explicitly (vmcnt) before the barrier that publishes a stage.
-// M0 is a reserved register the compiler does not track through asm clobbers;
-// this kernel has no other M0 user (no compiler-issued LDS copies, dynamic
-// register indexing or messages), so the asm owns it.
-// The code arrays are read once per decode and go out with the non-temporal
-// hint (streaming reads measured ~8% faster with it); the scale rows keep the
-// default policy, as the other kv-head group of the split reads the rest of
-// each 128-byte scale line from the same L2.
-template <bool NT>
-__device__ __forceinline__ void dma16(const uint8_t* sbase, uint32_t voff, uint32_t lds_dst) {
-  if constexpr (NT)
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase),
-                 "s"(lds_dst)
-                 : "memory");
-  else
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_dst)
-                 : "memory");
-}
-
-// ---------------------------------------------------------- code -> fp16 ---
-//
-// A code c placed at bit b (b + width <= 10) of an fp16 whose exponent field
-// is that of 1.0 reads as v = 1 + c/F with F = 2^(10 - b), and
-// (c - mid) = F (v - OFF), OFF = 1 + mid/F.  Codes go to the top mantissa bits
-// (F = 64 for INT4, 4 or 16 for INT2) so that the sums of v keep the bits the
-// result needs.  (Codes left in place as fp16 subnormals would save shifts,
-// but the matrix core does not multiply subnormal operands exactly against
-// operands of wide exponent range.)  One shift per distinct distance plus one
-// AND-OR per fp16 pair; the masks live in VGPRs (a three-operand VALU op may
-// read only one scalar).
-struct Masks {
-  uint32_t m47;  // bits 4-7 of both halves (INT4, F = 64)
-  uint32_t m89;  // bits 8-9 (INT2, F = 4)
-  uint32_t m67;  // bits 6-7 (INT2, F = 16)
-};
-
-__device__ __forceinline__ Masks make_masks(uint32_t opaque_zero) {
-  return Masks{0x00F000F0u | opaque_zero, 0x03000300u | opaque_zero, 0x00C000C0u | opaque_zero};
-}
-
-// (x & m) | 1.0-pairs as one v_bitop3_b32 (truth table 0xEA = (a & b) | c): a
-// compiler builtin, so the hazard recognizer sees it like any VALU op.
-__device__ __forceinline__ uint32_t ao(uint32_t x, uint32_t m) { return __builtin_amdgcn_bitop3_b32(x, m, kF16One2, 0xEA); }
-
-// INT4 word x (nibbles n0..n7, n_i at bits 4i): fp16 slots s0..s7 hold
-// n0, n4, n1, n5, n2, n6, n3, n7 (slot s <-> nibble (s>>1) + 4(s&1)), F = 64.
-// The same routine serves K rows (nibble = dim) and transpose-read V words
-// (nibble = token row).
-__device__ __forceinline__ u32x4 unpack4(uint32_t x, const Masks& k) {
-  return u32x4{ao(x << 4, k.m47), ao(x, k.m47), ao(x >> 4, k.m47), ao(x >> 8, k.m47)};
-}
-
-// INT2 K word x (codes c0..c15, c_j at bits 2j): pairs (c_j, c_{j+8}) for
-// j = o..o+3 (o = 0 or 4); slot s = 2i + hi holds c_{o+i+8hi}.  Even j go to
-// bits 8-9 (F = 4), odd j to bits 6-7 (F = 16): F(s) = (s & 2) ? 16 : 4.
-__device__ __forceinline__ u32x4 unpack2(uint32_t x, int o, const Masks& k) {
-  if (o == 0) return u32x4{ao(x << 8, k.m89), ao(x << 4, k.m67), ao(x << 4, k.m89), ao(x, k.m67)};
-  return u32x4{ao(x, k.m89), ao(x >> 4, k.m67), ao(x >> 4, k.m89), ao(x >> 8, k.m67)};
-}
-
-// INT2 transpose-read word x (nibble rho = codes of dims 2j, 2j+1 of token
-// row rho): parity 0 takes the even-dim code (bits 4rho..4rho+1) to bits 8-9
-// (F = 4), parity 1 the odd one (bits 4rho+2..4rho+3) to bits 6-7 (F = 16);
-// slot s <-> row (s>>1) + 4(s&1).
-__device__ __forceinline__ u32x4 unpack2_tr(uint32_t x, int parity, const Masks& k) {
-  if (parity == 0) return u32x4{ao(x << 8, k.m89), ao(x << 4, k.m89), ao(x, k.m89), ao(x >> 4, k.m89)};
-  return u32x4{ao(x << 4, k.m67), ao(x, k.m67), ao(x >> 4, k.m67), ao(x >> 8, k.m67)};
-}
-
-// QK: the query operand of K slot s carries F(s) / G, so every product is
-// q * v(s) * F(s) / G, and the accumulator starts at -sum q' OFF(s);
-// then C = sum q (c - mid) / G.
-template <int BITS>
-constexpr float kQkG = BITS == 4 ? 64.0f : 4.0f;
-template <int BITS>
-__device__ __forceinline__ float qk_factor(int s) {
-  if (BITS == 4) return 1.0f;
-  return (s & 2) ? 4.0f : 1.0f;
-}
-template <int BITS>
-__device__ __forceinline__ float qk_off(int s) {
-  if (BITS == 4) return 1.125f;
-  return (s & 2) ? 1.125f : 1.5f;
-}
-
-// dim of QK MFMA m's slot s for lane group q
-template <int BITS>
-__device__ __forceinline__ int qk_dim(int m, int q, int s) {
-  if (BITS == 4) return 32 * q + 8 * m + (s >> 1) + 4 * (s & 1);
-  return 32 * q + 16 * (m >> 1) + 4 * (m & 1) + (s >> 1) + 8 * (s & 1);
-}
-
-// PV: V codes sit at one position per output tile (INT4: F = 64; INT2 parity
-// 0: F = 4, parity 1: F = 16), so out = F (C - sum_t W OFF); the correction
-// operand holds OFF in every slot (rows identical).
-__device__ __forceinline__ u32x4 off_operand(float off) {
-  const _Float16 h = static_cast<_Float16>(off);
-  const uint32_t w = pack_half2(h, h);
-  return u32x4{w, w, w, w};
-}
-
-// ---------------------------------------------------------------- cursor ---
-struct Cursor {
-  int u, blk, vb, sb0;
-};
-
-// Advance to the next stage holding at least one valid token; false at the
-// end of the split.  units[2i] / units[2i+1] = block id / clamped valid count
-// of the split's i-th attended block (LDS).  Wave-uniform.
-__device__ __forceinline__ bool next_stage(Cursor& c, const int* units, int n_units) {
-  c.sb0 += kStageTok;
-  while (c.sb0 >= c.vb) {
-    if (++c.u >= n_units) return false;
-    c.blk = __builtin_amdgcn_readfirstlane(units[2 * c.u]);
-    c.vb = __builtin_amdgcn_readfirstlane(units[2 * c.u + 1]);
-    c.sb0 = 0;
-  }
-  return true;
 }
 
 // Per-lane byte offsets (relative to the stage's group base) of this wave's
@@ -322,62 +163,6 @@ __device__ __forceinline__ int w_chunk(int quad, int R, int c, int w, int half) 
     // own region after both stage buffers, [wave][quad][row][8 chunks]
     const int rp = R ^ ((R >> 2) & 1);
     return quad * 2048 + rp * 128 + 16 * (c ^ ((rp >> 1) & 7));
-  }
-}
-
-// ----------------------------------------------------------- query set-up ---
-template <int QUADS, int QSPLIT>
-struct QueryOps {
-  u32x4 qa[QUADS][QSPLIT][4];
-  f32x4 qcorr[QUADS];
-  float kscale[QUADS];
-};
-
-template <int BITS, int QUADS, int QSPLIT, typename QT>
-__device__ __forceinline__ void setup_query(QueryOps<QUADS, QSPLIT>& qo, const StagedParams& p, int head0, int li,
-                                            int lq) {
-#pragma unroll
-  for (int quad = 0; quad < QUADS; ++quad) {
-    // per-head power-of-two normaliser (exact): |q| * 2^-e in [1, 2)
-    const int hrow = quad * 4 + lq;
-    const int hrow_c = hrow < p.gq ? hrow : p.gq - 1;
-    float mx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(load_query<QT>(p.query, (head0 + hrow_c) * 128 + 8 * li + i)));
-    mx = row_max16(mx);
-    int ex = 0;
-    if (mx > 0.0f && isfinite(mx)) {
-      frexpf(mx, &ex);
-      ex -= 1;
-    }
-    qo.kscale[quad] = kQkG<BITS> * p.scale_log2 * exp2f(static_cast<float>(ex));
-    // A operand: lane row (h', g') = (li/4, li%4), non-zero when g' == lane group
-    const int ha = quad * 4 + (li >> 2);
-    const int ha_c = ha < p.gq ? ha : p.gq - 1;
-    const int e_a = __shfl(ex, (li >> 2) << 4, kWave);
-    const bool live = (li & 3) == lq && ha < p.gq;
-    float part = 0.0f;  // sum over this lane's row entries of (hi + lo) * OFF
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      _Float16 hi[8], lo[8];
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float raw = load_query<QT>(p.query, (head0 + ha_c) * 128 + qk_dim<BITS>(m, lq, s));
-        const float x = live ? ldexpf(raw, -e_a) * qk_factor<BITS>(s) : 0.0f;
-        hi[s] = static_cast<_Float16>(x);
-        lo[s] = QSPLIT == 2 ? static_cast<_Float16>(x - static_cast<float>(hi[s])) : static_cast<_Float16>(0.0f);
-        part += (static_cast<float>(hi[s]) + static_cast<float>(lo[s])) * qk_off<BITS>(s);
-      }
-      qo.qa[quad][0][m] = u32x4{pack_half2(hi[0], hi[1]), pack_half2(hi[2], hi[3]), pack_half2(hi[4], hi[5]),
-                                pack_half2(hi[6], hi[7])};
-      if (QSPLIT == 2)
-        qo.qa[quad][QSPLIT - 1][m] = u32x4{pack_half2(lo[0], lo[1]), pack_half2(lo[2], lo[3]),
-                                           pack_half2(lo[4], lo[5]), pack_half2(lo[6], lo[7])};
-    }
-    // C init of lane (li, lq), register g: row (h = lq, g) -> the lane holding
-    // that A row's non-zero entries is (li = 4 lq + g, group g)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) qo.qcorr[quad][g] = -__shfl(part, 16 * g + 4 * lq + g, kWave);
   }
 }
 
@@ -506,8 +291,7 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
   // --------------------------------------------------------------- softmax
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
-    float mx = fmaxf(fmaxf(score[quad][0], score[quad][1]), fmaxf(score[quad][2], score[quad][3]));
-    mx = row_max16(mx);
+    const float mx = row_max16_of(score[quad][0], score[quad][1], score[quad][2], score[quad][3]);
     const float m_new = fmaxf(st.m_run[quad], mx);
     const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m_run[quad] - m_new);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -516,13 +300,15 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
 #pragma unroll
     for (int tau = 0; tau < 4; ++tau) pr[tau] = __builtin_amdgcn_exp2f(score[quad][tau] - m_use);
     st.l_run[quad] = st.l_run[quad] * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-    // W = p * scale_v in fp16, masked tokens carry scale 0
+    // W = p * scale_v in fp16, masked tokens carry scale 0; INT4 tiles 0, 1
+    // sit in the K slots with F = 1024, so their W carries F/64 = 16
     uint32_t wlo[4], whi[4];  // per group g: (tile 0, tile 1), (tile 2, tile 3)
 #pragma unroll
     for (int tau = 0; tau < 4; tau += 2) {
       const bool ok0 = score[quad][tau] != -INFINITY;
       const bool ok1 = score[quad][tau + 1] != -INFINITY;
-      const float p0 = pr[tau], p1 = pr[tau + 1];
+      const float wfac = (BITS == 4 && tau == 0) ? 16.0f : 1.0f;
+      const float p0 = pr[tau] * wfac, p1 = pr[tau + 1] * wfac;
       const uint32_t a01 = ok0 ? svw[tau][0] : 0u, a23 = ok0 ? svw[tau][1] : 0u;
       const uint32_t b01 = ok1 ? svw[tau + 1][0] : 0u, b23 = ok1 ? svw[tau + 1][1] : 0u;
       const uint32_t w0 = pack_half2(static_cast<_Float16>(p0 * half_lo(a01)), static_cast<_Float16>(p1 * half_lo(b01)));
@@ -540,13 +326,14 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
       const int off = w_chunk<BITS, QUADS>(quad, 4 * lq + g, u >> 1, w, half) + 8 * (u & 1);
       *reinterpret_cast<u32x2*>(wbase + off) = u32x2{wlo[g], whi[g]};
     }
-    // rescale the PV state of column head li/4 by that head's alpha
-    const float a_pv = __shfl(alpha, (li >> 2) << 4, kWave);
-    if (__any(a_pv != 1.0f)) {
+    // rescale the PV state of column head li/4 by that head's alpha (alpha
+    // is uniform over each row: head h in lanes 16h .. 16h+15)
+    const RowValue a_pv = row_value(alpha, li >> 2);
+    if (a_pv.any_not_one) {
 #pragma unroll
-      for (int n = 0; n < 8; ++n) st.acc[quad][n] *= a_pv;
+      for (int n = 0; n < 8; ++n) st.acc[quad][n] *= a_pv.v;
 #pragma unroll
-      for (int c = 0; c < NPAR; ++c) st.corr[quad][c] *= a_pv;
+      for (int c = 0; c < NPAR; ++c) st.corr[quad][c] *= a_pv.v;
     }
   }
   // -------------------------------------------------------------------- PV
@@ -631,7 +418,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   __syncthreads();
 
   Cursor cur{-1, 0, 0, -kStageTok};
-  bool have = next_stage(cur, units, n_units);
+  bool have = next_stage<kStageTok>(cur, units, n_units);
   if (have && !(spec && cur.u == 0 && cur.sb0 == 0)) {
     // the first valid stage is elsewhere: let this wave's early copies land
     // (they target the same LDS chunks), then load the right ones
@@ -639,13 +426,17 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     issue_stage<BITS>(p, lds0, cur, kvh0, wave, cm);
   }
 
+  // query operands, through per-wave scratch in the second stage buffer (its
+  // first copies go out after the loop's first barrier)
   QueryOps<QUADS, QSPLIT> qo;
-  setup_query<BITS, QUADS, QSPLIT, QT>(qo, p, head0, li, lq);
+  static_assert(kWaves * coop_scratch_bytes<QUADS> <= G::STAGE, "query scratch fits a stage buffer");
+  coop_query<BITS, QUADS, QSPLIT, QT>(qo, p.query, p.gq, p.scale_log2, head0, lane,
+                                      lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
   // masks in VGPRs: p.units >= 1, so (lane & (p.units >> 30)) is 0 but opaque
   const Masks mk = make_masks(static_cast<uint32_t>(lane) & static_cast<uint32_t>(p.units >> 30));
   u32x4 offa[BITS == 4 ? 1 : 2];
   if (BITS == 4) {
-    offa[0] = off_operand(1.125f);
+    offa[0] = off_operand4();
   } else {
     offa[0] = off_operand(1.5f);
     offa[BITS == 4 ? 0 : 1] = off_operand(1.125f);
@@ -666,7 +457,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // the stage after the current one is looked up a step ahead, so that its
   // copies go out right after the barrier
   Cursor nxt = cur;
-  bool have_n = have && next_stage(nxt, units, n_units);
+  bool have_n = have && next_stage<kStageTok>(nxt, units, n_units);
   int buf = 0;
   while (have) {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
@@ -680,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     }
     cur = nxt;
     have = have_n;
-    if (have) have_n = next_stage(nxt, units, n_units);
+    if (have) have_n = next_stage<kStageTok>(nxt, units, n_units);
     buf ^= 1;
   }
 

@@ -1,0 +1,377 @@
+// Device helpers shared by the LDS-staged matrix-core decode kernels
+// (decode_staged.hip, decode_pairs.hip): operand types, the global -> LDS
+// copies, the in-register code -> fp16 unpack, the QK query operands and the
+// stage cursor.
+#pragma once
+
+#include "decode.hpp"
+
+namespace kvssd {
+namespace {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// ------------------------------------------------------------ small helpers
+
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, a), __builtin_bit_cast(half8_t, b), c, 0,
+                                                0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, lo)) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
+}
+
+__device__ __forceinline__ float half_lo(uint32_t x) { return half_bits_to_float(static_cast<uint16_t>(x & 0xFFFFu)); }
+__device__ __forceinline__ float half_hi(uint32_t x) { return half_bits_to_float(static_cast<uint16_t>(x >> 16)); }
+
+// LDS byte address of a pointer into a __shared__ array
+__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)p));
+}
+
+// ds_read_b64_tr_b4: within each group of 16 lanes, lane j receives nibble j of
+// the 8 bytes every lane of the group addressed, lane r's nibble landing in
+// bits 4r..4r+3 (a 16x16 nibble transpose).
+__device__ __forceinline__ i32x2 lds_read_tr4(const uint8_t* lds, int offset) {
+  typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+  return __builtin_amdgcn_ds_read_tr4_b64_v2i32((lds_i32x2*)(lds + offset));
+}
+
+// One global -> LDS copy instruction: lane i's 16 bytes from sbase + voff land
+// at LDS byte lds_dst + 16 i.  Issued from asm so that the compiler does not
+// treat it as a pending write to every LDS location: in its intrinsic form the
+// compiler waits for all outstanding copies (i.e. the next stage's prefetch)
+// before any LDS read it cannot tell apart from them.  The copies' completion
+// is awaited explicitly (vmcnt) before a stage is read.
+// M0 is a reserved register the compiler does not track through asm clobbers;
+// the kernels using these copies have no other M0 user (no compiler-issued
+// LDS copies, dynamic register indexing or messages), so the asm owns it.
+// NT: non-temporal hint, for the code arrays, read once per decode (streaming
+// reads measured ~8% faster with it).  Scale rows keep the default policy:
+// other workgroups of the split read the rest of each 128-byte scale line
+// from the same L2.
+template <bool NT>
+__device__ __forceinline__ void dma16(const uint8_t* sbase, uint32_t voff, uint32_t lds_dst) {
+  if constexpr (NT)
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase),
+                 "s"(lds_dst)
+                 : "memory");
+  else
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_dst)
+                 : "memory");
+}
+
+// As dma16 with 4 bytes per lane: lane i's dword lands at LDS byte lds_dst + 4 i.
+__device__ __forceinline__ void dma4(const uint8_t* sbase, uint32_t voff, uint32_t lds_dst) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_dst)
+               : "memory");
+}
+
+// ---------------------------------------------------------- code -> fp16 ---
+//
+// A code c placed at bit b (b + width <= 10) of an fp16 whose exponent field
+// is that of 1.0 reads as v = 1 + c/F with F = 2^(10 - b), and
+// (c - mid) = F (v - OFF), OFF = 1 + mid/F.  Codes stay in the normal range
+// (codes left in place as fp16 subnormals would save shifts, but the matrix
+// core does not multiply subnormal operands exactly against operands of wide
+// exponent range).  One shift per distinct distance plus one AND-OR per fp16
+// pair; the masks live in VGPRs (a three-operand VALU op may read only one
+// scalar).  The factor F(s) of each MFMA K slot is exact (a power of two) and
+// is carried by the other operand: by the query in QK, by W in PV.
+struct Masks {
+  uint32_t m03;  // bits 0-3 of both halves (INT4, F = 1024)
+  uint32_t m47;  // bits 4-7 (INT4, F = 64)
+  uint32_t m89;  // bits 8-9 (INT2, F = 4)
+  uint32_t m67;  // bits 6-7 (INT2, F = 16)
+};
+
+__device__ __forceinline__ Masks make_masks(uint32_t opaque_zero) {
+  return Masks{0x000F000Fu | opaque_zero, 0x00F000F0u | opaque_zero, 0x03000300u | opaque_zero,
+               0x00C000C0u | opaque_zero};
+}
+
+// (x & m) | 1.0-pairs as one v_bitop3_b32 (truth table 0xEA = (a & b) | c): a
+// compiler builtin, so the hazard recognizer sees it like any VALU op.
+__device__ __forceinline__ uint32_t ao(uint32_t x, uint32_t m) { return __builtin_amdgcn_bitop3_b32(x, m, kF16One2, 0xEA); }
+
+// INT4 word x (nibbles n0..n7, n_i at bits 4i): fp16 slots s0..s7 hold
+// n0, n4, n1, n5, n2, n6, n3, n7 (slot s <-> nibble (s>>1) + 4(s&1)) with one
+// shift: n0, n4, n2, n6 stay at bits 0-3 of their half (F = 1024), n1, n5,
+// n3, n7 at bits 4-7 (F = 64), i.e. F(s) = 1024 for s in {0, 1, 4, 5}.  The
+// same routine serves K rows (nibble = dim) and transpose-read V words
+// (nibble = token row).
+__device__ __forceinline__ u32x4 unpack4(uint32_t x, const Masks& k) {
+  const uint32_t y = x >> 8;
+  return u32x4{ao(x, k.m03), ao(x, k.m47), ao(y, k.m03), ao(y, k.m47)};
+}
+
+// INT4 slot s holds its code at F = 1024 (else F = 64)
+constexpr bool fine_slot4(int s) { return ((s >> 1) & 1) == 0; }
+
+// INT2 K word x (codes c0..c15, c_j at bits 2j): pairs (c_j, c_{j+8}) for
+// j = o..o+3 (o = 0 or 4); slot s = 2i + hi holds c_{o+i+8hi}.  Even j go to
+// bits 8-9 (F = 4), odd j to bits 6-7 (F = 16): F(s) = (s & 2) ? 16 : 4.
+__device__ __forceinline__ u32x4 unpack2(uint32_t x, int o, const Masks& k) {
+  if (o == 0) return u32x4{ao(x << 8, k.m89), ao(x << 4, k.m67), ao(x << 4, k.m89), ao(x, k.m67)};
+  return u32x4{ao(x, k.m89), ao(x >> 4, k.m67), ao(x >> 4, k.m89), ao(x >> 8, k.m67)};
+}
+
+// INT2 transpose-read word x (nibble rho = codes of dims 2j, 2j+1 of token
+// row rho): parity 0 takes the even-dim code (bits 4rho..4rho+1) to bits 8-9
+// (F = 4), parity 1 the odd one (bits 4rho+2..4rho+3) to bits 6-7 (F = 16);
+// slot s <-> row (s>>1) + 4(s&1).
+__device__ __forceinline__ u32x4 unpack2_tr(uint32_t x, int parity, const Masks& k) {
+  if (parity == 0) return u32x4{ao(x << 8, k.m89), ao(x << 4, k.m89), ao(x, k.m89), ao(x >> 4, k.m89)};
+  return u32x4{ao(x << 4, k.m67), ao(x, k.m67), ao(x >> 4, k.m67), ao(x >> 8, k.m67)};
+}
+
+// QK: the query operand of K slot s carries F(s) / G, so every product is
+// q * v(s) * F(s) / G, and the accumulator starts at -sum q' OFF(s);
+// then C = sum q (c - mid) / G.
+template <int BITS>
+constexpr float kQkG = BITS == 4 ? 64.0f : 4.0f;
+template <int BITS>
+__device__ __forceinline__ float qk_factor(int s) {
+  if (BITS == 4) return fine_slot4(s) ? 16.0f : 1.0f;
+  return (s & 2) ? 4.0f : 1.0f;
+}
+template <int BITS>
+__device__ __forceinline__ float qk_off(int s) {
+  if (BITS == 4) return fine_slot4(s) ? 1.0078125f : 1.125f;
+  return (s & 2) ? 1.125f : 1.5f;
+}
+
+// dim of QK MFMA m's slot s for lane group q
+template <int BITS>
+__device__ __forceinline__ int qk_dim(int m, int q, int s) {
+  if (BITS == 4) return 32 * q + 8 * m + (s >> 1) + 4 * (s & 1);
+  return 32 * q + 16 * (m >> 1) + 4 * (m & 1) + (s >> 1) + 8 * (s & 1);
+}
+
+// PV: INT2 V codes sit at one position per output tile (parity 0: F = 4,
+// parity 1: F = 16), so out = F (C - sum_t W OFF); the correction operand
+// holds OFF in every slot (rows identical).  INT4 V codes sit at F(s) per K
+// slot; W of slot s carries F(s)/64, the correction operand OFF(s), and
+// out = 64 (C - sum_t W' OFF).
+__device__ __forceinline__ u32x4 off_operand(float off) {
+  const _Float16 h = static_cast<_Float16>(off);
+  const uint32_t w = pack_half2(h, h);
+  return u32x4{w, w, w, w};
+}
+__device__ __forceinline__ u32x4 off_operand4() {
+  const _Float16 f = static_cast<_Float16>(qk_off<4>(0)), c = static_cast<_Float16>(qk_off<4>(2));
+  const uint32_t wf = pack_half2(f, f), wc = pack_half2(c, c);
+  return u32x4{wf, wc, wf, wc};
+}
+
+// ---------------------------------------------------------- row reductions
+// max over the 16 lanes of each row of max(a, b, c, d) (pass b = c = d = a
+// for fewer inputs), in every lane: v_max_f32 with DPP row rotations.  (The
+// compiler's form of a DPP reduction moves the operand through a separate DPP
+// mov and canonicalises it: four instructions a step.)  s_nop 1 before each
+// DPP read covers the VALU-write -> DPP-read hazard (two wait states);
+// nothing in the sequence involves the matrix core.
+__device__ __forceinline__ float row_max16_of(float a, float b, float c, float d) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3\n\t"
+      "v_max_f32 %0, %0, %4\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:2 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_f32_dpp %0, %0, %0 row_ror:1 row_mask:0xf bank_mask:0xf"
+      : "=&v"(r)
+      : "v"(a), "v"(b), "v"(c), "v"(d));
+  return r;
+}
+
+// A value uniform over each 16-lane row (row h = lanes 16h .. 16h+15), read
+// by every lane for row hsel, and whether any row differs from 1.0 (scalar):
+// the four row values go through SGPRs instead of an LDS permute.
+struct RowValue {
+  float v;
+  bool any_not_one;
+};
+__device__ __forceinline__ RowValue row_value(float x, int hsel) {
+  constexpr int kOne = 0x3F800000;
+  const int a0 = __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 0);
+  const int a1 = __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 16);
+  const int a2 = __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 32);
+  const int a3 = __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 48);
+  const bool any = ((a0 ^ kOne) | (a1 ^ kOne) | (a2 ^ kOne) | (a3 ^ kOne)) != 0;
+  const int v = hsel == 0 ? a0 : hsel == 1 ? a1 : hsel == 2 ? a2 : a3;
+  return RowValue{__builtin_bit_cast(float, v), any};
+}
+
+// ---------------------------------------------------------------- cursor ---
+struct Cursor {
+  int u, blk, vb, sb0;
+};
+
+// Advance to the next stage (STAGE_TOK tokens) holding at least one valid token; false at the
+// end of the split.  units[2i] / units[2i+1] = block id / clamped valid count
+// of the split's i-th attended block (LDS).  Wave-uniform.
+template <int STAGE_TOK>
+__device__ __forceinline__ bool next_stage(Cursor& c, const int* units, int n_units) {
+  c.sb0 += STAGE_TOK;
+  while (c.sb0 >= c.vb) {
+    if (++c.u >= n_units) return false;
+    c.blk = __builtin_amdgcn_readfirstlane(units[2 * c.u]);
+    c.vb = __builtin_amdgcn_readfirstlane(units[2 * c.u + 1]);
+    c.sb0 = 0;
+  }
+  return true;
+}
+
+// ----------------------------------------------------------- query set-up ---
+template <int QUADS, int QSPLIT>
+struct QueryOps {
+  u32x4 qa[QUADS][QSPLIT][4];
+  f32x4 qcorr[QUADS];
+  float kscale[QUADS];
+};
+
+// Query operands of the kv head whose first query head is head0 (gq query
+// heads per kv head, QUADS = ceil(gq / 4) groups of 4), for QK lane (li, lq).
+template <int BITS, int QUADS, int QSPLIT, typename QT>
+__device__ __forceinline__ void setup_query(QueryOps<QUADS, QSPLIT>& qo, const void* query, int gq, float scale_log2,
+                                            int head0, int li, int lq) {
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    // per-head power-of-two normaliser (exact): |q| * 2^-e in [1, 2)
+    const int hrow = quad * 4 + lq;
+    const int hrow_c = hrow < gq ? hrow : gq - 1;
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(load_query<QT>(query, (head0 + hrow_c) * 128 + 8 * li + i)));
+    mx = row_max16(mx);
+    int ex = 0;
+    if (mx > 0.0f && isfinite(mx)) {
+      frexpf(mx, &ex);
+      ex -= 1;
+    }
+    qo.kscale[quad] = kQkG<BITS> * scale_log2 * exp2f(static_cast<float>(ex));
+    // A operand: lane row (h', g') = (li/4, li%4), non-zero when g' == lane group
+    const int ha = quad * 4 + (li >> 2);
+    const int ha_c = ha < gq ? ha : gq - 1;
+    const int e_a = __shfl(ex, (li >> 2) << 4, kWave);
+    const bool live = (li & 3) == lq && ha < gq;
+    float part = 0.0f;  // sum over this lane's row entries of (hi + lo) * OFF
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      _Float16 hi[8], lo[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float raw = load_query<QT>(query, (head0 + ha_c) * 128 + qk_dim<BITS>(m, lq, s));
+        const float x = live ? ldexpf(raw, -e_a) * qk_factor<BITS>(s) : 0.0f;
+        hi[s] = static_cast<_Float16>(x);
+        lo[s] = QSPLIT == 2 ? static_cast<_Float16>(x - static_cast<float>(hi[s])) : static_cast<_Float16>(0.0f);
+        part += (static_cast<float>(hi[s]) + static_cast<float>(lo[s])) * qk_off<BITS>(s);
+      }
+      qo.qa[quad][0][m] = u32x4{pack_half2(hi[0], hi[1]), pack_half2(hi[2], hi[3]), pack_half2(hi[4], hi[5]),
+                                pack_half2(hi[6], hi[7])};
+      if (QSPLIT == 2)
+        qo.qa[quad][QSPLIT - 1][m] = u32x4{pack_half2(lo[0], lo[1]), pack_half2(lo[2], lo[3]),
+                                           pack_half2(lo[4], lo[5]), pack_half2(lo[6], lo[7])};
+    }
+    // C init of lane (li, lq), register g: row (h = lq, g) -> the lane holding
+    // that A row's non-zero entries is (li = 4 lq + g, group g)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) qo.qcorr[quad][g] = -__shfl(part, 16 * g + 4 * lq + g, kWave);
+  }
+}
+
+// As setup_query, with every value converted once: the query operands of the
+// kv head are built through LDS scratch of the calling wave
+// (coop_scratch_bytes, 16-byte aligned).  Writer lane L = 16h + 4q + m forms
+// slot group (m, q) of query head h (of each quad) -- the 8 dims
+// qk_dim(m, q, .) -- then every A-operand lane (li, lq) reads its rows back.
+// Stores are unconditional, one slot per lane: a store under a lane condition
+// to an address other lanes share may be compiled as a read-select-write by
+// every lane, and the lanes then race.
+template <int QUADS>
+constexpr int coop_scratch_bytes = QUADS * 2560;
+
+template <int BITS, int QUADS, int QSPLIT, typename QT>
+__device__ __forceinline__ void coop_query(QueryOps<QUADS, QSPLIT>& qo, const void* query, int gq, float scale_log2,
+                                           int head0, int lane, uint8_t* scratch) {
+  const int li = lane & 15, lq = lane >> 4;
+  const int h = lane >> 4, q = (lane >> 2) & 3, m = lane & 3;
+  uint8_t* hi_s = scratch;                                               // [quad][head][q][m] x 16 B
+  uint8_t* lo_s = scratch + QUADS * 1024;                                // same, lo parts
+  float* corr_s = reinterpret_cast<float*>(scratch + QUADS * 2048);      // [quad][head][lane16]
+  float* ksc_s = corr_s + QUADS * 64;                                    // [quad][head][lane16]
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    const int hq = quad * 4 + h;
+    const bool have = hq < gq;
+    const int base = (head0 + (have ? hq : 0)) * 128;
+    float x[8];
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) x[sl] = have ? load_query<QT>(query, base + qk_dim<BITS>(m, q, sl)) : 0.0f;
+    float mx = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) mx = fmaxf(mx, fabsf(x[sl]));
+    mx = row_max16(mx);  // over the head's 128 dims
+    int ex = 0;
+    if (mx > 0.0f && isfinite(mx)) {
+      frexpf(mx, &ex);
+      ex -= 1;
+    }
+    _Float16 hi[8], lo[8];
+    float part = 0.0f;  // sum over the slot group of (hi + lo) * OFF
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl) {
+      const float y = ldexpf(x[sl], -ex) * qk_factor<BITS>(sl);
+      hi[sl] = static_cast<_Float16>(y);
+      lo[sl] = QSPLIT == 2 ? static_cast<_Float16>(y - static_cast<float>(hi[sl])) : static_cast<_Float16>(0.0f);
+      part += (static_cast<float>(hi[sl]) + static_cast<float>(lo[sl])) * qk_off<BITS>(sl);
+    }
+    const int slot = ((quad * 4 + h) * 16 + (lane & 15)) * 16;
+    *reinterpret_cast<u32x4*>(hi_s + slot) =
+        u32x4{pack_half2(hi[0], hi[1]), pack_half2(hi[2], hi[3]), pack_half2(hi[4], hi[5]), pack_half2(hi[6], hi[7])};
+    if (QSPLIT == 2)
+      *reinterpret_cast<u32x4*>(lo_s + slot) =
+          u32x4{pack_half2(lo[0], lo[1]), pack_half2(lo[2], lo[3]), pack_half2(lo[4], lo[5]), pack_half2(lo[6], lo[7])};
+    // group q = the 4 lanes m = 0..3
+    part += __shfl_xor(part, 1, kWave);
+    part += __shfl_xor(part, 2, kWave);
+    corr_s[(quad * 4 + h) * 16 + (lane & 15)] = part;
+    ksc_s[(quad * 4 + h) * 16 + (lane & 15)] = kQkG<BITS> * scale_log2 * exp2f(static_cast<float>(ex));
+  }
+  // (one wave wrote, the same wave reads: LDS keeps its order)
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    // A row (head li/4, group li%4) is non-zero only in lane group lq == li%4
+    // (rows of absent heads were written as zeros)
+    const bool live = (li & 3) == lq;
+    const int row = ((quad * 4 + (li >> 2)) * 16 + 4 * lq) * 16;
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(hi_s + row + 16 * mm);
+      qo.qa[quad][0][mm] = live ? v : u32x4{0u, 0u, 0u, 0u};
+      if (QSPLIT == 2) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(lo_s + row + 16 * mm);
+        qo.qa[quad][QSPLIT - 1][mm] = live ? w : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    // C init of QK lane (li, lq), register g: row (head lq, group g), the sum
+    // held by lane 4g of the writer row
+#pragma unroll
+    for (int g = 0; g < 4; ++g) qo.qcorr[quad][g] = -corr_s[(quad * 4 + lq) * 16 + 4 * g];
+    qo.kscale[quad] = ksc_s[(quad * 4 + lq) * 16];
+  }
+}
+
+
+}  // namespace
+}  // namespace kvssd
