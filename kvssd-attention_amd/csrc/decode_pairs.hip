@@ -300,6 +300,11 @@ __global__ __launch_bounds__(kPThreads) void decode_pairs_kernel(PairParams p) {
     }
   }
 
+  // the query loads go out next: they complete in issue order, right after
+  // the first stage's copies, instead of a round trip after them
+  const QueryRaw<1> qraw0 = coop_query_load<4, 1, QT>(p.query, p.gq, kvh * p.gq, lane);
+  const QueryRaw<1> qraw1 = coop_query_load<4, 1, QT>(p.query, p.gq, (kvh + 1) * p.gq, lane);
+
   // the split's (block id, clamped valid count) list, read once into LDS
   int* units = reinterpret_cast<int*>(lds + kPWaves * kWaveBytes);
   const int n_units = max(0, u_end - u_begin);  // <= kPMaxUnits, checked on the host
@@ -323,10 +328,8 @@ __global__ __launch_bounds__(kPThreads) void decode_pairs_kernel(PairParams p) {
   // out in the loop, after these LDS accesses are done)
   QueryOps<1, QSPLIT> qo[2];
   static_assert(2 * coop_scratch_bytes<1> <= kBufBytes, "query scratch fits a buffer");
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh)
-    coop_query<4, 1, QSPLIT, QT>(qo[hh], p.query, p.gq, p.scale_log2, (kvh + hh) * p.gq, lane,
-                                 wlds + kBufBytes + hh * coop_scratch_bytes<1>);
+  coop_query_build<4, 1, QSPLIT>(qo[0], qraw0, p.scale_log2, lane, wlds + kBufBytes);
+  coop_query_build<4, 1, QSPLIT>(qo[1], qraw1, p.scale_log2, lane, wlds + kBufBytes + coop_scratch_bytes<1>);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   // masks in VGPRs: p.units >= 1, so (lane & (p.units >> 30)) is 0 but opaque
   const Masks mk = make_masks(static_cast<uint32_t>(lane) & static_cast<uint32_t>(p.units >> 30));

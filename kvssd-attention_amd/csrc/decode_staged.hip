@@ -407,6 +407,10 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     }
   }
 
+  // the query loads go out next: they complete in issue order, right after
+  // the first stage's copies, instead of a round trip after them
+  const QueryRaw<QUADS> qraw = coop_query_load<BITS, QUADS, QT>(p.query, p.gq, head0, lane);
+
   // the split's (block id, clamped valid count) list, read once into LDS
   int* units = reinterpret_cast<int*>(lds + 2 * G::STAGE + kWBytes);
   const int n_units = max(0, u_end - u_begin);  // <= kMaxUnits, checked on the host
@@ -430,8 +434,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // first copies go out after the loop's first barrier)
   QueryOps<QUADS, QSPLIT> qo;
   static_assert(kWaves * coop_scratch_bytes<QUADS> <= G::STAGE, "query scratch fits a stage buffer");
-  coop_query<BITS, QUADS, QSPLIT, QT>(qo, p.query, p.gq, p.scale_log2, head0, lane,
-                                      lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
+  coop_query_build<BITS, QUADS, QSPLIT>(qo, qraw, p.scale_log2, lane, lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
   // masks in VGPRs: p.units >= 1, so (lane & (p.units >> 30)) is 0 but opaque
   const Masks mk = make_masks(static_cast<uint32_t>(lane) & static_cast<uint32_t>(p.units >> 30));
   u32x4 offa[BITS == 4 ? 1 : 2];

@@ -301,23 +301,41 @@ __device__ __forceinline__ void setup_query(QueryOps<QUADS, QSPLIT>& qo, const v
 template <int QUADS>
 constexpr int coop_scratch_bytes = QUADS * 2560;
 
-template <int BITS, int QUADS, int QSPLIT, typename QT>
-__device__ __forceinline__ void coop_query(QueryOps<QUADS, QSPLIT>& qo, const void* query, int gq, float scale_log2,
-                                           int head0, int lane, uint8_t* scratch) {
-  const int li = lane & 15, lq = lane >> 4;
+// The two phases of coop_query: the loads (issued early, so that their
+// latency overlaps the first stage's copies) and the build.
+template <int QUADS>
+struct QueryRaw {
+  float x[QUADS][8];  // writer lane's slot group, per quad
+};
+
+template <int BITS, int QUADS, typename QT>
+__device__ __forceinline__ QueryRaw<QUADS> coop_query_load(const void* query, int gq, int head0, int lane) {
   const int h = lane >> 4, q = (lane >> 2) & 3, m = lane & 3;
+  QueryRaw<QUADS> r;
+#pragma unroll
+  for (int quad = 0; quad < QUADS; ++quad) {
+    const int hq = quad * 4 + h;
+    const bool have = hq < gq;
+    const int base = (head0 + (have ? hq : 0)) * 128;
+#pragma unroll
+    for (int sl = 0; sl < 8; ++sl)
+      r.x[quad][sl] = have ? load_query<QT>(query, base + qk_dim<BITS>(m, q, sl)) : 0.0f;
+  }
+  return r;
+}
+
+template <int BITS, int QUADS, int QSPLIT>
+__device__ __forceinline__ void coop_query_build(QueryOps<QUADS, QSPLIT>& qo, const QueryRaw<QUADS>& r,
+                                                 float scale_log2, int lane, uint8_t* scratch) {
+  const int li = lane & 15, lq = lane >> 4;
+  const int h = lane >> 4;
   uint8_t* hi_s = scratch;                                               // [quad][head][q][m] x 16 B
   uint8_t* lo_s = scratch + QUADS * 1024;                                // same, lo parts
   float* corr_s = reinterpret_cast<float*>(scratch + QUADS * 2048);      // [quad][head][lane16]
   float* ksc_s = corr_s + QUADS * 64;                                    // [quad][head][lane16]
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
-    const int hq = quad * 4 + h;
-    const bool have = hq < gq;
-    const int base = (head0 + (have ? hq : 0)) * 128;
-    float x[8];
-#pragma unroll
-    for (int sl = 0; sl < 8; ++sl) x[sl] = have ? load_query<QT>(query, base + qk_dim<BITS>(m, q, sl)) : 0.0f;
+    const float* x = r.x[quad];
     float mx = 0.0f;
 #pragma unroll
     for (int sl = 0; sl < 8; ++sl) mx = fmaxf(mx, fabsf(x[sl]));
@@ -370,6 +388,13 @@ __device__ __forceinline__ void coop_query(QueryOps<QUADS, QSPLIT>& qo, const vo
     for (int g = 0; g < 4; ++g) qo.qcorr[quad][g] = -corr_s[(quad * 4 + lq) * 16 + 4 * g];
     qo.kscale[quad] = ksc_s[(quad * 4 + lq) * 16];
   }
+}
+
+template <int BITS, int QUADS, int QSPLIT, typename QT>
+__device__ __forceinline__ void coop_query(QueryOps<QUADS, QSPLIT>& qo, const void* query, int gq, float scale_log2,
+                                           int head0, int lane, uint8_t* scratch) {
+  coop_query_build<BITS, QUADS, QSPLIT>(qo, coop_query_load<BITS, QUADS, QT>(query, gq, head0, lane), scale_log2,
+                                        lane, scratch);
 }
 
 
