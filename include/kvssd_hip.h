@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KVSSD_HIP_ABI_VERSION 1
+#define KVSSD_HIP_ABI_VERSION 2
 
 /* Query element types accepted by kvssd_hip_fused_decode (the reference
  * dispatches fp32/fp64/fp16/bf16 queries: csrc/fused_decode.cu:131-133). */
@@ -137,6 +137,48 @@ int kvssd_hip_unpack_codes(const uint8_t* packed, int bits, int64_t n_bytes, uin
  * Twin of dequantize_tensor (src/kvssd/quant.py:94-99); exact. */
 int kvssd_hip_dequantize(const uint8_t* packed, const uint16_t* scales, int64_t rows, int head_dim, int bits,
                          int group_size, float* out, void* stream);
+
+/* Shape of a v1 KV block record: the CacheSpec fields that lay it out
+ * (src/kvssd/format.py:23-58). */
+typedef struct kvssd_record_layout {
+  int32_t bits;
+  int32_t block_tokens;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t group_size;
+} kvssd_record_layout;
+
+/* Bytes of one record: the 52-byte header plus the payload, padded to a 4096
+ * multiple (CacheSpec.record_bytes, src/kvssd/format.py:53-58). */
+int kvssd_hip_record_bytes(const kvssd_record_layout* layout, size_t* bytes);
+
+/* `n` raw records in device memory, `stride` bytes apart (4-byte aligned),
+ * into the PackedBatch arrays: packed_k/v [n, BT, KVH, PD], scales_k/v fp16
+ * [n, BT, KVH, G], valid [n] (the header's valid tokens), and status [n]:
+ * 0 ok, 1 invalid header (magic or version), 2 layout differs from `layout`,
+ * 3 payload length or CRC-32 mismatch (checked when verify_crc != 0).
+ * The GPU form of decode_record (src/kvssd/format.py:134-177) over a span of
+ * records, replacing the loader's payload clones and the pipeline's per-array
+ * stacking (src/kvssd/loader.py:73-91, src/kvssd/pipeline.py:98-108). */
+int kvssd_hip_gather_records(const kvssd_record_layout* layout, const uint8_t* records, size_t stride, int n,
+                             int verify_crc, uint8_t* packed_k, uint8_t* packed_v, uint16_t* scales_k,
+                             uint16_t* scales_v, int32_t* valid, int32_t* status, void* stream);
+
+/* Groupwise quantisation of `rows` rows of `head_dim` values of `dtype`
+ * (kvssd_dtype): packed [rows, head_dim*bits/8] (low bits first), fp16 scales
+ * [rows, head_dim/group_size].  Bit-exact twin of quantize_tensor
+ * (src/kvssd/quant.py:49-65). */
+int kvssd_hip_quantize(const void* x, int dtype, int64_t rows, int head_dim, int bits, int group_size,
+                       uint8_t* packed, uint16_t* scales, void* stream);
+
+/* Records of one layer: keys and values [tokens, KVH, D] of `dtype` become
+ * ceil(tokens / BT) records (record_bytes each) for blocks first_block,
+ * first_block + 1, ... -- the last block zero-padded -- and their payload
+ * CRC-32 in crcs.  KVCacheStore.create's block loop (src/kvssd/store.py:46-63)
+ * with encode_record (src/kvssd/format.py:104-131), on the GPU. */
+int kvssd_hip_encode_records(const kvssd_record_layout* layout, int dtype, const void* keys, const void* values,
+                             int64_t tokens, int layer, int first_block, uint8_t* records, uint32_t* crcs,
+                             void* stream);
 
 /* hipMemcpyAsync host->device of `bytes` bytes on `stream`; `src` should be
  * page-locked for the copy to be asynchronous.  The staging copy of

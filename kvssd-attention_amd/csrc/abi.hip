@@ -260,6 +260,33 @@ __attribute__((visibility("default"))) int kvssd_hip_dequantize(const uint8_t* p
   return launch_dequantize(packed, scales, rows, head_dim, bits, group_size, out, static_cast<hipStream_t>(stream));
 }
 
+__attribute__((visibility("default"))) int kvssd_hip_record_bytes(const kvssd_record_layout* layout, size_t* bytes) {
+  return record_bytes_of(layout, bytes);
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_gather_records(
+    const kvssd_record_layout* layout, const uint8_t* records, size_t stride, int n, int verify_crc,
+    uint8_t* packed_k, uint8_t* packed_v, uint16_t* scales_k, uint16_t* scales_v, int32_t* valid, int32_t* status,
+    void* stream) {
+  return launch_gather_records(layout, records, stride, n, verify_crc, packed_k, packed_v, scales_k, scales_v, valid,
+                               status, static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_quantize(const void* x, int dtype, int64_t rows, int head_dim,
+                                                              int bits, int group_size, uint8_t* packed,
+                                                              uint16_t* scales, void* stream) {
+  return launch_quantize(x, dtype, rows, head_dim, bits, group_size, packed, scales,
+                         static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_encode_records(const kvssd_record_layout* layout, int dtype,
+                                                                    const void* keys, const void* values,
+                                                                    int64_t tokens, int layer, int first_block,
+                                                                    uint8_t* records, uint32_t* crcs, void* stream) {
+  return launch_encode_records(layout, dtype, keys, values, tokens, layer, first_block, records, crcs,
+                               static_cast<hipStream_t>(stream));
+}
+
 __attribute__((visibility("default"))) int kvssd_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes,
                                                                       void* stream) {
   if (bytes == 0) return 0;

@@ -53,6 +53,16 @@ int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int he
 // ---- chunk merge (pipeline), codec twins
 int launch_merge_chunks(int rows, int dim, float* acc_out, float* acc_lse, const float* out, const float* lse,
                         hipStream_t stream);
+// ---- record codec (records.hip)
+int record_bytes_of(const kvssd_record_layout* layout, size_t* bytes);
+int launch_gather_records(const kvssd_record_layout* layout, const uint8_t* records, size_t stride, int n,
+                          int verify_crc, uint8_t* packed_k, uint8_t* packed_v, uint16_t* scales_k,
+                          uint16_t* scales_v, int32_t* valid, int32_t* status, hipStream_t stream);
+int launch_quantize(const void* x, int dtype, int64_t rows, int head_dim, int bits, int group_size, uint8_t* packed,
+                    uint16_t* scales, hipStream_t stream);
+int launch_encode_records(const kvssd_record_layout* layout, int dtype, const void* keys, const void* values,
+                          int64_t tokens, int layer, int first_block, uint8_t* records, uint32_t* crcs,
+                          hipStream_t stream);
 int launch_unpack_codes(const uint8_t* packed, int bits, int64_t n_bytes, uint8_t* codes, hipStream_t stream);
 int launch_dequantize(const uint8_t* packed, const uint16_t* scales, int64_t rows, int head_dim, int bits,
                       int group_size, float* out, hipStream_t stream);

@@ -1,0 +1,442 @@
+// GPU codec of the v1 KV block record (src/kvssd/format.py:14-177):
+//
+// * gather: raw records (as read from the store, copied to HBM in one span)
+//   -> the PackedBatch arrays, with decode_record's header, layout and
+//   payload CRC-32 checks (format.py:134-177); replaces the loader's per-block
+//   payload clones and the pipeline's per-array stacking
+//   (src/kvssd/loader.py:73-91, src/kvssd/pipeline.py:98-108);
+// * quantize: bit-exact twin of quantize_tensor (src/kvssd/quant.py:49-65);
+// * encode: KVCacheStore.create's block loop for one layer (zero-padded last
+//   block, src/kvssd/store.py:46-63) -- quantise keys and values and write
+//   whole records with their CRC-32 (encode_record, format.py:104-131).
+//
+// CRC-32 is zlib's: reflected polynomial 0xEDB88320, register preset to all
+// ones, output complemented.  Polynomials over GF(2) are held bit-reflected
+// (bit 31 is the coefficient of x^0).  The raw register update (preset 0, no
+// complement) is linear, so with crc_raw(A || B) = x^(8|B|) crc_raw(A) + crc_raw(B)
+// (mod P) a record's payload is split into 1024 equal segments, one per thread,
+// each run through a slicing-by-4 table walk, and the segment values are
+// folded pairwise in 10 levels.  Leading zero bytes do not change crc_raw, so
+// a payload that does not split evenly is virtually left-padded with zeros.
+// Finally crc32(D) = x^(8|D|) * 0xFFFFFFFF + crc_raw(D) + 0xFFFFFFFF.
+#include "decode.hpp"
+
+namespace kvssd {
+namespace {
+
+constexpr uint32_t kPoly = 0xEDB88320u;
+constexpr int kHeaderBytes = 52;      // "<8sIIIIIIIIIII"
+constexpr int kRecordAlign = 4096;
+constexpr uint32_t kMagic0 = 0x5353564Bu;  // "KVSS", little-endian
+constexpr uint32_t kMagic1 = 0x31303044u;  // "D001"
+constexpr int kCrcThreads = 1024;          // segments per record
+constexpr int kCrcLevels = 10;             // log2(kCrcThreads)
+
+// a * b mod P (reflected representation)
+__host__ __device__ constexpr uint32_t gf_mul(uint32_t a, uint32_t b) {
+  uint32_t p = 0;
+  for (int i = 0; i < 32; ++i) {
+    if (a & (0x80000000u >> i)) p ^= b;
+    b = (b & 1u) ? (b >> 1) ^ kPoly : b >> 1;  // b *= x
+  }
+  return p;
+}
+
+// x^(8 n) mod P
+__host__ __device__ constexpr uint32_t x_pow_bytes(uint64_t n) {
+  uint32_t r = 0x80000000u;   // x^0
+  uint32_t sq = 0x00800000u;  // x^8
+  while (n) {
+    if (n & 1u) r = gf_mul(r, sq);
+    sq = gf_mul(sq, sq);
+    n >>= 1;
+  }
+  return r;
+}
+
+// raw register after byte n followed by k zero bytes (slicing-by-4 table k)
+__device__ __forceinline__ uint32_t crc_table_entry(int k, uint32_t n) {
+  uint32_t c = n;
+  for (int i = 0; i < 8 * (k + 1); ++i) c = (c & 1u) ? (c >> 1) ^ kPoly : c >> 1;
+  return c;
+}
+
+struct CrcPlan {
+  uint32_t seg_bytes;           // L: bytes per segment (multiple of 4)
+  uint32_t pad;                 // virtual leading zero bytes
+  uint32_t len;                 // payload bytes covered
+  uint32_t x_len;               // x^(8 len) mod P
+  uint32_t level[kCrcLevels];   // x^(8 L 2^k) mod P
+};
+
+CrcPlan make_crc_plan(uint32_t len) {
+  CrcPlan c{};
+  const uint32_t per = (len + kCrcThreads - 1) / kCrcThreads;
+  c.seg_bytes = (per + 3u) & ~3u;
+  c.pad = c.seg_bytes * kCrcThreads - len;
+  c.len = len;
+  c.x_len = x_pow_bytes(len);
+  for (int k = 0; k < kCrcLevels; ++k) c.level[k] = x_pow_bytes(static_cast<uint64_t>(c.seg_bytes) << k);
+  return c;
+}
+
+// zlib CRC-32 of data[0 .. plan.len), data 4-byte aligned; every thread of a
+// kCrcThreads workgroup calls it; tab = the four slicing tables in LDS,
+// seg = kCrcThreads words of LDS.  Returns the CRC in every thread.
+__device__ uint32_t block_crc32(const uint8_t* data, const CrcPlan& plan, const uint32_t (*tab)[256], uint32_t* seg) {
+  const int tid = threadIdx.x;
+  const int64_t v0 = static_cast<int64_t>(tid) * plan.seg_bytes - plan.pad;  // first real byte of the segment
+  uint32_t crc = 0;
+  if ((plan.len & 3u) == 0) {
+    // pad is then a multiple of 4: whole dwords, real or virtual zeros
+    for (uint32_t i = 0; i < plan.seg_bytes; i += 4) {
+      const int64_t at = v0 + i;
+      if (at < 0) continue;  // leading zeros keep the raw register at 0
+      crc ^= *reinterpret_cast<const uint32_t*>(data + at);
+      crc = tab[3][crc & 0xFFu] ^ tab[2][(crc >> 8) & 0xFFu] ^ tab[1][(crc >> 16) & 0xFFu] ^ tab[0][crc >> 24];
+    }
+  } else {
+    for (uint32_t i = 0; i < plan.seg_bytes; ++i) {
+      const int64_t at = v0 + i;
+      if (at < 0) continue;
+      crc = tab[0][(crc ^ data[at]) & 0xFFu] ^ (crc >> 8);
+    }
+  }
+  seg[tid] = crc;
+  for (int k = 0; k < kCrcLevels; ++k) {
+    __syncthreads();
+    const int span = 1 << k;
+    if ((tid & (2 * span - 1)) == 0) seg[tid] = gf_mul(plan.level[k], seg[tid]) ^ seg[tid + span];
+  }
+  __syncthreads();
+  const uint32_t raw = seg[0];
+  __syncthreads();  // seg may be reused by the caller
+  return gf_mul(plan.x_len, 0xFFFFFFFFu) ^ raw ^ 0xFFFFFFFFu;
+}
+
+__device__ __forceinline__ void fill_crc_tables(uint32_t (*tab)[256]) {
+  for (int i = threadIdx.x; i < 4 * 256; i += blockDim.x) tab[i >> 8][i & 255] = crc_table_entry(i >> 8, i & 255);
+}
+
+// bytes [0, len) from src to dst, dwords when both ends allow
+__device__ __forceinline__ void copy_region(const uint8_t* src, uint8_t* dst, int64_t len) {
+  if (((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) | static_cast<uintptr_t>(len)) & 3u) == 0) {
+    const uint32_t* s = reinterpret_cast<const uint32_t*>(src);
+    uint32_t* d = reinterpret_cast<uint32_t*>(dst);
+    for (int64_t i = threadIdx.x; i < len / 4; i += blockDim.x) d[i] = s[i];
+  } else {
+    for (int64_t i = threadIdx.x; i < len; i += blockDim.x) dst[i] = src[i];
+  }
+}
+
+struct Layout {
+  int bits, block_tokens, kv_heads, head_dim, group_size;
+  __host__ __device__ int64_t scale_bytes() const { return static_cast<int64_t>(block_tokens) * kv_heads * (head_dim / group_size) * 2; }
+  __host__ __device__ int64_t packed_bytes() const { return static_cast<int64_t>(block_tokens) * kv_heads * head_dim * bits / 8; }
+  __host__ __device__ int64_t payload_bytes() const { return 2 * scale_bytes() + 2 * packed_bytes(); }
+  __host__ __device__ int64_t record_bytes() const {
+    const int64_t n = kHeaderBytes + payload_bytes();
+    return (n + kRecordAlign - 1) / kRecordAlign * kRecordAlign;
+  }
+};
+
+// ------------------------------------------------------------------ gather ---
+struct GatherParams {
+  const uint8_t* records;
+  int64_t stride;
+  int n, verify;
+  Layout lay;
+  CrcPlan plan;
+  uint8_t *pk, *pv, *sk, *sv;
+  int32_t* valid;
+  int32_t* status;
+};
+
+// one workgroup per record; status: 0 ok, 1 invalid header (magic / version),
+// 2 layout differs from the expected one, 3 payload length or CRC mismatch
+__global__ __launch_bounds__(kCrcThreads) void gather_records_kernel(GatherParams p) {
+  __shared__ uint32_t tab[4][256];
+  __shared__ uint32_t seg[kCrcThreads];
+  __shared__ uint32_t hdr[kHeaderBytes / 4];
+  const int r = blockIdx.x;
+  const uint8_t* rec = p.records + static_cast<int64_t>(r) * p.stride;
+  fill_crc_tables(tab);
+  if (threadIdx.x < kHeaderBytes / 4) hdr[threadIdx.x] = reinterpret_cast<const uint32_t*>(rec)[threadIdx.x];
+  __syncthreads();
+  int status = 0;
+  if (hdr[0] != kMagic0 || hdr[1] != kMagic1 || hdr[2] != 1u) {
+    status = 1;
+  } else if (hdr[6] != static_cast<uint32_t>(p.lay.bits) || hdr[7] != static_cast<uint32_t>(p.lay.block_tokens) ||
+             hdr[8] != static_cast<uint32_t>(p.lay.kv_heads) || hdr[9] != static_cast<uint32_t>(p.lay.head_dim) ||
+             hdr[10] != static_cast<uint32_t>(p.lay.group_size)) {
+    status = 2;
+  }
+  const int64_t s = p.lay.scale_bytes(), pb = p.lay.packed_bytes();
+  const uint8_t* pay = rec + kHeaderBytes;
+  copy_region(pay, p.sk + r * s, s);
+  copy_region(pay + s, p.sv + r * s, s);
+  copy_region(pay + 2 * s, p.pk + r * pb, pb);
+  copy_region(pay + 2 * s + pb, p.pv + r * pb, pb);
+  if (p.verify && status == 0) {
+    // a record written for this layout has exactly the layout's payload
+    if (hdr[11] != p.plan.len) {
+      status = 3;
+    } else {
+      const uint32_t crc = block_crc32(pay, p.plan, tab, seg);
+      if (crc != hdr[12]) status = 3;
+    }
+  }
+  if (threadIdx.x == 0) {
+    p.status[r] = status;
+    p.valid[r] = static_cast<int32_t>(hdr[5]);
+  }
+}
+
+// ---------------------------------------------------------------- quantize ---
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+  return static_cast<float>(v);
+}
+template <>
+__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) {  // bfloat16 bits
+  return __builtin_bit_cast(float, static_cast<uint32_t>(v) << 16);
+}
+
+// one group (group_size consecutive values) -> packed bytes + fp16 scale, as
+// quantize_tensor: scale32 = max|x| (at least 1e-8) / (2^(bits-1) - 1) with
+// IEEE division, code = clamp(rint(x / scale32), -mid, mid - 1) + mid, codes
+// packed low bits first, scale stored as fp16 (round to nearest even).  A
+// null src reads zeros (padding tokens).
+template <typename T>
+__device__ __forceinline__ void quantize_group(const T* src, int group_size, int bits, uint8_t* packed, uint16_t* scale) {
+  float amax = 0.0f;
+  for (int i = 0; i < group_size; ++i) amax = fmaxf(amax, fabsf(src ? to_f32(src[i]) : 0.0f));
+  const int mid = 1 << (bits - 1);
+  const float s32 = fmaxf(amax, 1e-8f) / static_cast<float>(mid - 1);
+  const int per = 8 / bits;
+  for (int b = 0; b < group_size / per; ++b) {
+    uint32_t byte = 0;
+    for (int j = 0; j < per; ++j) {
+      const float x = src ? to_f32(src[b * per + j]) : 0.0f;
+      const float c = fminf(fmaxf(rintf(x / s32), static_cast<float>(-mid)), static_cast<float>(mid - 1));
+      byte |= static_cast<uint32_t>(static_cast<int>(c) + mid) << (j * bits);
+    }
+    packed[b] = static_cast<uint8_t>(byte);
+  }
+  *scale = __builtin_bit_cast(uint16_t, static_cast<_Float16>(s32));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ x, int64_t groups, int group_size, int bits,
+                                                       uint8_t* __restrict__ packed, uint16_t* __restrict__ scales) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= groups) return;
+  quantize_group(x + g * group_size, group_size, bits, packed + g * (group_size * bits / 8), scales + g);
+}
+
+// ------------------------------------------------------------------ encode ---
+struct EncodeParams {
+  const void* keys;
+  const void* values;
+  int64_t tokens;
+  int n, layer, first_block;
+  Layout lay;
+  CrcPlan plan;
+  uint8_t* records;
+  uint32_t* crcs;
+};
+
+// phase 1: every (record, key/value, token, kv head, group) quantised into
+// the record's payload; tokens past the end read as zeros
+template <typename T>
+__global__ __launch_bounds__(256) void encode_payload_kernel(EncodeParams p) {
+  const Layout& L = p.lay;
+  const int G = L.head_dim / L.group_size;
+  const int64_t per_record = static_cast<int64_t>(L.block_tokens) * L.kv_heads * G;  // groups per array
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= 2 * per_record * p.n) return;
+  const int r = static_cast<int>(g / (2 * per_record));
+  const int64_t rest = g % (2 * per_record);
+  const bool is_v = rest >= per_record;
+  const int64_t q = is_v ? rest - per_record : rest;  // (token, head, group) within the block
+  const int64_t row = q / G;                          // token * kv_heads + head
+  const int gi = static_cast<int>(q % G);
+  const int64_t token = static_cast<int64_t>(r) * L.block_tokens + row / L.kv_heads;
+  const T* base = static_cast<const T*>(is_v ? p.values : p.keys);
+  const T* src = token < p.tokens ? base + (token * L.kv_heads + row % L.kv_heads) * L.head_dim + gi * L.group_size
+                                  : nullptr;
+  uint8_t* pay = p.records + static_cast<int64_t>(r) * L.record_bytes() + kHeaderBytes;
+  const int64_t s = L.scale_bytes(), pb = L.packed_bytes();
+  uint16_t* scale = reinterpret_cast<uint16_t*>(pay + (is_v ? s : 0)) + q;
+  uint8_t* packed = pay + 2 * s + (is_v ? pb : 0) + q * (L.group_size * L.bits / 8);
+  quantize_group(src, L.group_size, L.bits, packed, scale);
+}
+
+// phase 2: one workgroup per record -- CRC of the payload, header, padding
+__global__ __launch_bounds__(kCrcThreads) void encode_header_kernel(EncodeParams p) {
+  __shared__ uint32_t tab[4][256];
+  __shared__ uint32_t seg[kCrcThreads];
+  const Layout& L = p.lay;
+  const int r = blockIdx.x;
+  uint8_t* rec = p.records + static_cast<int64_t>(r) * L.record_bytes();
+  fill_crc_tables(tab);
+  __syncthreads();
+  const uint32_t crc = block_crc32(rec + kHeaderBytes, p.plan, tab, seg);
+  const int64_t start = static_cast<int64_t>(r) * L.block_tokens;
+  const int64_t valid = p.tokens - start < L.block_tokens ? p.tokens - start : L.block_tokens;
+  if (threadIdx.x < kHeaderBytes / 4) {
+    uint32_t v = 0;
+    switch (threadIdx.x) {
+      case 0: v = kMagic0; break;
+      case 1: v = kMagic1; break;
+      case 2: v = 1u; break;
+      case 3: v = static_cast<uint32_t>(p.layer); break;
+      case 4: v = static_cast<uint32_t>(p.first_block + r); break;
+      case 5: v = static_cast<uint32_t>(valid); break;
+      case 6: v = static_cast<uint32_t>(L.bits); break;
+      case 7: v = static_cast<uint32_t>(L.block_tokens); break;
+      case 8: v = static_cast<uint32_t>(L.kv_heads); break;
+      case 9: v = static_cast<uint32_t>(L.head_dim); break;
+      case 10: v = static_cast<uint32_t>(L.group_size); break;
+      case 11: v = p.plan.len; break;
+      default: v = crc; break;
+    }
+    reinterpret_cast<uint32_t*>(rec)[threadIdx.x] = v;
+  }
+  for (int64_t i = kHeaderBytes + L.payload_bytes() + threadIdx.x; i < L.record_bytes(); i += blockDim.x) rec[i] = 0;
+  if (threadIdx.x == 0) p.crcs[r] = crc;
+}
+
+int check_layout(const kvssd_record_layout* l, Layout* out) {
+  if (l == nullptr) return arg_error("record layout is NULL");
+  if (l->bits != 2 && l->bits != 4) return arg_error("bits must be 2 or 4");
+  if (l->block_tokens <= 0 || l->kv_heads <= 0 || l->head_dim <= 0)
+    return arg_error("all cache dimensions must be positive");
+  if (l->group_size <= 0 || l->head_dim % l->group_size) return arg_error("head_dim must be divisible by group_size");
+  if (l->group_size % (8 / l->bits)) return arg_error("group_size must be positive and pack-aligned");
+  *out = Layout{l->bits, l->block_tokens, l->kv_heads, l->head_dim, l->group_size};
+  if (out->payload_bytes() > 0x7FFFFFFFLL) return arg_error("record payload too large");
+  return 0;
+}
+
+template <typename T>
+void launch_quantize_t(const void* x, int64_t groups, int group_size, int bits, uint8_t* packed, uint16_t* scales,
+                       hipStream_t s) {
+  const int64_t blocks = (groups + 255) / 256;
+  hipLaunchKernelGGL(quantize_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, static_cast<const T*>(x),
+                     groups, group_size, bits, packed, scales);
+}
+
+template <typename T>
+void launch_encode_t(const EncodeParams& p, hipStream_t s) {
+  const int64_t groups = 2LL * p.lay.block_tokens * p.lay.kv_heads * (p.lay.head_dim / p.lay.group_size) * p.n;
+  hipLaunchKernelGGL(encode_payload_kernel<T>, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0, s, p);
+}
+
+}  // namespace
+
+int record_bytes_of(const kvssd_record_layout* layout, size_t* bytes) {
+  Layout L{};
+  if (int rc = check_layout(layout, &L)) return rc;
+  if (bytes == nullptr) return arg_error("bytes output pointer is NULL");
+  *bytes = static_cast<size_t>(L.record_bytes());
+  return 0;
+}
+
+int launch_gather_records(const kvssd_record_layout* layout, const uint8_t* records, size_t stride, int n,
+                          int verify_crc, uint8_t* packed_k, uint8_t* packed_v, uint16_t* scales_k,
+                          uint16_t* scales_v, int32_t* valid, int32_t* status, hipStream_t stream) {
+  Layout L{};
+  if (int rc = check_layout(layout, &L)) return rc;
+  if (n < 0) return arg_error("record count must be non-negative");
+  if (n == 0) return 0;
+  if (!records || !packed_k || !packed_v || !scales_k || !scales_v || !valid || !status)
+    return arg_error("a required buffer pointer is NULL");
+  if (stride < static_cast<size_t>(L.record_bytes()) || (stride % 4) || (reinterpret_cast<uintptr_t>(records) % 4))
+    return arg_error("records must be 4-byte aligned and at least record_bytes apart");
+  GatherParams p{};
+  p.records = records;
+  p.stride = static_cast<int64_t>(stride);
+  p.n = n;
+  p.verify = verify_crc != 0;
+  p.lay = L;
+  p.plan = make_crc_plan(static_cast<uint32_t>(L.payload_bytes()));
+  p.pk = packed_k;
+  p.pv = packed_v;
+  p.sk = reinterpret_cast<uint8_t*>(scales_k);
+  p.sv = reinterpret_cast<uint8_t*>(scales_v);
+  p.valid = valid;
+  p.status = status;
+  hipLaunchKernelGGL(gather_records_kernel, dim3(static_cast<unsigned>(n)), dim3(kCrcThreads), 0, stream, p);
+  return hip_status(hipGetLastError(), "gather_records launch");
+}
+
+int launch_quantize(const void* x, int dtype, int64_t rows, int head_dim, int bits, int group_size, uint8_t* packed,
+                    uint16_t* scales, hipStream_t stream) {
+  if (bits != 2 && bits != 4) return arg_error("bits must be 2 or 4");
+  if (group_size <= 0 || group_size % (8 / bits)) return arg_error("group_size must be positive and pack-aligned");
+  if (head_dim <= 0 || head_dim % group_size) return arg_error("last dimension must be divisible by group_size");
+  if (rows < 0) return arg_error("row count must be non-negative");
+  if (rows == 0) return 0;
+  if (!x || !packed || !scales) return arg_error("a required buffer pointer is NULL");
+  const int64_t groups = rows * (head_dim / group_size);
+  switch (dtype) {
+    case KVSSD_DTYPE_F16:
+      launch_quantize_t<_Float16>(x, groups, group_size, bits, packed, scales, stream);
+      break;
+    case KVSSD_DTYPE_BF16:
+      launch_quantize_t<uint16_t>(x, groups, group_size, bits, packed, scales, stream);
+      break;
+    case KVSSD_DTYPE_F32:
+      launch_quantize_t<float>(x, groups, group_size, bits, packed, scales, stream);
+      break;
+    case KVSSD_DTYPE_F64:
+      launch_quantize_t<double>(x, groups, group_size, bits, packed, scales, stream);
+      break;
+    default:
+      return arg_error("quantization input must be floating point");
+  }
+  return hip_status(hipGetLastError(), "quantize launch");
+}
+
+int launch_encode_records(const kvssd_record_layout* layout, int dtype, const void* keys, const void* values,
+                          int64_t tokens, int layer, int first_block, uint8_t* records, uint32_t* crcs,
+                          hipStream_t stream) {
+  Layout L{};
+  if (int rc = check_layout(layout, &L)) return rc;
+  if (tokens < 0) return arg_error("token count must be non-negative");
+  if (tokens == 0) return 0;
+  if (!keys || !values || !records || !crcs) return arg_error("a required buffer pointer is NULL");
+  EncodeParams p{};
+  p.keys = keys;
+  p.values = values;
+  p.tokens = tokens;
+  p.n = static_cast<int>((tokens + L.block_tokens - 1) / L.block_tokens);
+  p.layer = layer;
+  p.first_block = first_block;
+  p.lay = L;
+  p.plan = make_crc_plan(static_cast<uint32_t>(L.payload_bytes()));
+  p.records = records;
+  p.crcs = crcs;
+  switch (dtype) {
+    case KVSSD_DTYPE_F16:
+      launch_encode_t<_Float16>(p, stream);
+      break;
+    case KVSSD_DTYPE_BF16:
+      launch_encode_t<uint16_t>(p, stream);
+      break;
+    case KVSSD_DTYPE_F32:
+      launch_encode_t<float>(p, stream);
+      break;
+    case KVSSD_DTYPE_F64:
+      launch_encode_t<double>(p, stream);
+      break;
+    default:
+      return arg_error("quantization input must be floating point");
+  }
+  if (int rc = hip_status(hipGetLastError(), "encode_records launch")) return rc;
+  hipLaunchKernelGGL(encode_header_kernel, dim3(static_cast<unsigned>(p.n)), dim3(kCrcThreads), 0, stream, p);
+  return hip_status(hipGetLastError(), "encode_records launch");
+}
+
+}  // namespace kvssd

@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "libkvssd_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_GENERAL, KERNEL_MFMA, KERNEL_STAGED, KERNEL_PAIRS = 0, 1, 2, 3, 4
@@ -52,6 +52,12 @@ class DecodeDesc(ctypes.Structure):
     ]
 
 
+class RecordLayout(ctypes.Structure):
+    """kvssd_record_layout (include/kvssd_hip.h)."""
+
+    _fields_ = [(n, ctypes.c_int32) for n in ("bits", "block_tokens", "kv_heads", "head_dim", "group_size")]
+
+
 # (name, restype, argtypes) for every entry point in include/kvssd_hip.h
 _VP, _SZ, _I, _I64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int64
 SIGNATURES = {
@@ -65,6 +71,10 @@ SIGNATURES = {
     "kvssd_hip_merge_chunks": (_I, [_I, _I, _VP, _VP, _VP, _VP, _VP]),
     "kvssd_hip_unpack_codes": (_I, [_VP, _I, _I64, _VP, _VP]),
     "kvssd_hip_dequantize": (_I, [_VP, _VP, _I64, _I, _I, _I, _VP, _VP]),
+    "kvssd_hip_record_bytes": (_I, [ctypes.POINTER(RecordLayout), ctypes.POINTER(_SZ)]),
+    "kvssd_hip_gather_records": (_I, [ctypes.POINTER(RecordLayout), _VP, _SZ, _I, _I] + [_VP] * 7),
+    "kvssd_hip_quantize": (_I, [_VP, _I, _I64, _I, _I, _I, _VP, _VP, _VP]),
+    "kvssd_hip_encode_records": (_I, [ctypes.POINTER(RecordLayout), _I, _VP, _VP, _I64, _I, _I, _VP, _VP, _VP]),
     "kvssd_hip_memcpy_h2d_async": (_I, [_VP, _VP, _SZ, _VP]),
     "kvssd_hip_last_error": (ctypes.c_char_p, []),
 }
