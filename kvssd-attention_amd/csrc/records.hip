@@ -13,12 +13,21 @@
 // CRC-32 is zlib's: reflected polynomial 0xEDB88320, register preset to all
 // ones, output complemented.  Polynomials over GF(2) are held bit-reflected
 // (bit 31 is the coefficient of x^0).  The raw register update (preset 0, no
-// complement) is linear, so with crc_raw(A || B) = x^(8|B|) crc_raw(A) + crc_raw(B)
-// (mod P) a record's payload is split into 1024 equal segments, one per thread,
-// each run through a slicing-by-4 table walk, and the segment values are
-// folded pairwise in 10 levels.  Leading zero bytes do not change crc_raw, so
-// a payload that does not split evenly is virtually left-padded with zeros.
-// Finally crc32(D) = x^(8|D|) * 0xFFFFFFFF + crc_raw(D) + 0xFFFFFFFF.
+// complement) is linear: crc_raw(A || B) = x^(8|B|) crc_raw(A) + crc_raw(B)
+// (mod P), and leading zero bytes do not change crc_raw, so a payload is
+// virtually left-padded with zeros to a whole number of pieces.  Finally
+// crc32(D) = x^(8|D|) * 0xFFFFFFFF + crc_raw(D) + 0xFFFFFFFF.
+//
+// Chunked form (layouts whose four payload arrays are 16-byte multiples, the
+// usual case): a workgroup of 1024 threads covers a record in 16-byte chunks,
+// chunk c = j * 1024 + t belonging to thread t.  Every thread issues all its
+// loads at once (coalesced), stores each chunk to its PackedBatch array and
+// takes the chunk's crc_raw from the registers with 16 independent table
+// lookups (slicing-by-16).  Its own chunks fold by Horner's rule with a
+// table-driven multiply by x^(8 * 16384); the 1024 thread values then fold
+// pairwise in 10 levels (x^(8 * 16 * 2^k)).  Other layouts take the general
+// form: 1024 contiguous segments through a slicing-by-4 walk, then the same
+// 10-level fold.  All tables are built at compile time.
 #include "decode.hpp"
 
 namespace kvssd {
@@ -54,12 +63,40 @@ __host__ __device__ constexpr uint32_t x_pow_bytes(uint64_t n) {
   return r;
 }
 
-// raw register after byte n followed by k zero bytes (slicing-by-4 table k)
-__device__ __forceinline__ uint32_t crc_table_entry(int k, uint32_t n) {
-  uint32_t c = n;
-  for (int i = 0; i < 8 * (k + 1); ++i) c = (c & 1u) ? (c >> 1) ^ kPoly : c >> 1;
-  return c;
+constexpr int kChunkBytes = 16;
+constexpr int kStrideBytes = kChunkBytes * kCrcThreads;  // one row of chunks
+constexpr int kMaxRows = 16;                             // chunked form: payload <= 256 KiB
+
+// slice[k][n]: raw register after byte n followed by k zero bytes;
+// horner[k][b]: x^(8 * kStrideBytes) * (b << 8k), so that the product with any
+// word is the XOR of four lookups
+struct CrcTables {
+  uint32_t slice[16][256];
+  uint32_t horner[4][256];
+};
+
+constexpr CrcTables make_crc_tables() {
+  CrcTables t{};
+  for (uint32_t n = 0; n < 256; ++n) {
+    uint32_t c = n;
+    for (int i = 0; i < 8; ++i) c = (c & 1u) ? (c >> 1) ^ kPoly : c >> 1;
+    t.slice[0][n] = c;
+  }
+  for (int k = 1; k < 16; ++k)
+    for (uint32_t n = 0; n < 256; ++n) {
+      const uint32_t c = t.slice[k - 1][n];
+      t.slice[k][n] = t.slice[0][c & 0xFFu] ^ (c >> 8);  // one more zero byte
+    }
+  const uint32_t m = x_pow_bytes(kStrideBytes);
+  for (int k = 0; k < 4; ++k)
+    for (uint32_t b = 0; b < 256; ++b) t.horner[k][b] = gf_mul(m, b << (8 * k));
+  return t;
 }
+
+__device__ const CrcTables kCrcTables = make_crc_tables();
+
+// raw register after byte n followed by k zero bytes (slicing-by-4 table k)
+__device__ __forceinline__ uint32_t crc_table_entry(int k, uint32_t n) { return kCrcTables.slice[k][n]; }
 
 struct CrcPlan {
   uint32_t seg_bytes;           // L: bytes per segment (multiple of 4)
@@ -116,6 +153,83 @@ __device__ uint32_t block_crc32(const uint8_t* data, const CrcPlan& plan, const 
 
 __device__ __forceinline__ void fill_crc_tables(uint32_t (*tab)[256]) {
   for (int i = threadIdx.x; i < 4 * 256; i += blockDim.x) tab[i >> 8][i & 255] = crc_table_entry(i >> 8, i & 255);
+}
+
+// ----------------------------------------------------------- chunked form ---
+struct ChunkLds {
+  uint32_t slice[16][256];
+  uint32_t horner[4][256];
+  uint32_t seg[kCrcThreads];
+};
+
+__device__ __forceinline__ void load_chunk_tables(ChunkLds& l) {
+  const uint32_t* src = &kCrcTables.slice[0][0];
+  uint32_t* dst = &l.slice[0][0];
+  for (int i = threadIdx.x; i < 20 * 256; i += kCrcThreads) dst[i] = src[i];  // slice then horner
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16 bytes at a 4-byte aligned address
+__device__ __forceinline__ u32x4 load16(const uint8_t* p) {
+  u32x4 v;
+  __builtin_memcpy(&v, __builtin_assume_aligned(p, 4), 16);
+  return v;
+}
+
+__device__ __forceinline__ uint32_t crc16_raw(const ChunkLds& l, u32x4 v) {
+  uint32_t c = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t x = v[w];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) c ^= l.slice[15 - 4 * w - b][(x >> (8 * b)) & 0xFFu];
+  }
+  return c;
+}
+
+__device__ __forceinline__ uint32_t mul_stride(const ChunkLds& l, uint32_t a) {
+  return l.horner[0][a & 0xFFu] ^ l.horner[1][(a >> 8) & 0xFFu] ^ l.horner[2][(a >> 16) & 0xFFu] ^
+         l.horner[3][a >> 24];
+}
+
+// Chunk geometry of a payload of `len` bytes (a multiple of 16): `rows` rows of
+// 1024 chunks, the first `pad` bytes virtual zeros.
+struct ChunkPlan {
+  int rows;
+  int64_t pad;
+  uint32_t level[kCrcLevels];  // x^(8 * 16 * 2^k) mod P
+  uint32_t x_len;              // x^(8 len) mod P
+};
+
+ChunkPlan make_chunk_plan(uint32_t len) {
+  ChunkPlan c{};
+  c.rows = static_cast<int>((len + kStrideBytes - 1) / kStrideBytes);
+  c.pad = static_cast<int64_t>(c.rows) * kStrideBytes - len;
+  c.x_len = x_pow_bytes(len);
+  for (int k = 0; k < kCrcLevels; ++k) c.level[k] = x_pow_bytes(static_cast<uint64_t>(kChunkBytes) << k);
+  return c;
+}
+
+// byte offset (into the payload) of chunk row j of this thread; negative = virtual zeros
+__device__ __forceinline__ int64_t chunk_offset(const ChunkPlan& c, int j) {
+  return (static_cast<int64_t>(j) * kCrcThreads + threadIdx.x) * kChunkBytes - c.pad;
+}
+
+// Fold this thread's Horner value `h` with every other thread's: the payload's
+// zlib CRC-32, returned in every thread.
+__device__ uint32_t fold_chunks(ChunkLds& l, const ChunkPlan& c, uint32_t h) {
+  const int tid = threadIdx.x;
+  l.seg[tid] = h;
+  for (int k = 0; k < kCrcLevels; ++k) {
+    __syncthreads();
+    const int span = 1 << k;
+    if ((tid & (2 * span - 1)) == 0) l.seg[tid] = gf_mul(c.level[k], l.seg[tid]) ^ l.seg[tid + span];
+  }
+  __syncthreads();
+  const uint32_t raw = l.seg[0];
+  __syncthreads();
+  return gf_mul(c.x_len, 0xFFFFFFFFu) ^ raw ^ 0xFFFFFFFFu;
 }
 
 // bytes [0, len) from src to dst, dwords when both ends allow
@@ -184,6 +298,68 @@ __global__ __launch_bounds__(kCrcThreads) void gather_records_kernel(GatherParam
     } else {
       const uint32_t crc = block_crc32(pay, p.plan, tab, seg);
       if (crc != hdr[12]) status = 3;
+    }
+  }
+  if (threadIdx.x == 0) {
+    p.status[r] = status;
+    p.valid[r] = static_cast<int32_t>(hdr[5]);
+  }
+}
+
+// chunked form of gather_records_kernel (same statuses), for layouts whose
+// four arrays are 16-byte multiples and 16-byte aligned destinations
+__global__ __launch_bounds__(kCrcThreads) void gather_chunked_kernel(GatherParams p, ChunkPlan c) {
+  __shared__ ChunkLds lds;
+  __shared__ uint32_t hdr[kHeaderBytes / 4];
+  const int r = blockIdx.x;
+  const uint8_t* rec = p.records + static_cast<int64_t>(r) * p.stride;
+  const uint8_t* pay = rec + kHeaderBytes;
+  u32x4 v[kMaxRows];
+#pragma unroll
+  for (int j = 0; j < kMaxRows; ++j) {
+    v[j] = u32x4{0u, 0u, 0u, 0u};
+    if (j < c.rows) {
+      const int64_t o = chunk_offset(c, j);
+      if (o >= 0) v[j] = load16(pay + o);
+    }
+  }
+  if (threadIdx.x < kHeaderBytes / 4) hdr[threadIdx.x] = reinterpret_cast<const uint32_t*>(rec)[threadIdx.x];
+  if (p.verify) load_chunk_tables(lds);
+  const int64_t sb = p.lay.scale_bytes(), pb = p.lay.packed_bytes();
+#pragma unroll
+  for (int j = 0; j < kMaxRows; ++j) {
+    if (j < c.rows) {
+      const int64_t o = chunk_offset(c, j);
+      if (o >= 0) {
+        uint8_t* dst;
+        if (o < sb) dst = p.sk + r * sb + o;
+        else if (o < 2 * sb) dst = p.sv + r * sb + (o - sb);
+        else if (o < 2 * sb + pb) dst = p.pk + r * pb + (o - 2 * sb);
+        else dst = p.pv + r * pb + (o - 2 * sb - pb);
+        *reinterpret_cast<u32x4*>(dst) = v[j];
+      }
+    }
+  }
+  __syncthreads();
+  int status = 0;
+  if (hdr[0] != kMagic0 || hdr[1] != kMagic1 || hdr[2] != 1u) {
+    status = 1;
+  } else if (hdr[6] != static_cast<uint32_t>(p.lay.bits) || hdr[7] != static_cast<uint32_t>(p.lay.block_tokens) ||
+             hdr[8] != static_cast<uint32_t>(p.lay.kv_heads) || hdr[9] != static_cast<uint32_t>(p.lay.head_dim) ||
+             hdr[10] != static_cast<uint32_t>(p.lay.group_size)) {
+    status = 2;
+  }
+  // status, p.verify and the header are the same in every thread, so the
+  // fold's barriers are reached by the whole workgroup or by none of it
+  if (p.verify && status == 0) {
+    if (hdr[11] != p.plan.len) {
+      status = 3;
+    } else {
+      uint32_t h = 0;
+#pragma unroll
+      for (int j = 0; j < kMaxRows; ++j)
+        if (j < c.rows) h = mul_stride(lds, h) ^ crc16_raw(lds, v[j]);
+      if (fold_chunks(lds, c, h) != hdr[12]) status = 3;
     }
   }
   if (threadIdx.x == 0) {
@@ -272,16 +448,39 @@ __global__ __launch_bounds__(256) void encode_payload_kernel(EncodeParams p) {
   quantize_group(src, L.group_size, L.bits, packed, scale);
 }
 
-// phase 2: one workgroup per record -- CRC of the payload, header, padding
-__global__ __launch_bounds__(kCrcThreads) void encode_header_kernel(EncodeParams p) {
-  __shared__ uint32_t tab[4][256];
-  __shared__ uint32_t seg[kCrcThreads];
+// phase 2: one workgroup per record -- CRC of the payload, header, padding.
+// CHUNKED: the payload is a 16-byte multiple of at most kMaxRows rows.
+template <bool CHUNKED>
+__global__ __launch_bounds__(kCrcThreads) void encode_header_kernel(EncodeParams p, ChunkPlan c) {
+  __shared__ ChunkLds lds;
   const Layout& L = p.lay;
   const int r = blockIdx.x;
   uint8_t* rec = p.records + static_cast<int64_t>(r) * L.record_bytes();
-  fill_crc_tables(tab);
-  __syncthreads();
-  const uint32_t crc = block_crc32(rec + kHeaderBytes, p.plan, tab, seg);
+  uint32_t crc;
+  if constexpr (CHUNKED) {
+    const uint8_t* pay = rec + kHeaderBytes;
+    u32x4 v[kMaxRows];
+#pragma unroll
+    for (int j = 0; j < kMaxRows; ++j) {
+      v[j] = u32x4{0u, 0u, 0u, 0u};
+      if (j < c.rows) {
+        const int64_t o = chunk_offset(c, j);
+        if (o >= 0) v[j] = load16(pay + o);
+      }
+    }
+    load_chunk_tables(lds);
+    __syncthreads();
+    uint32_t h = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxRows; ++j)
+      if (j < c.rows) h = mul_stride(lds, h) ^ crc16_raw(lds, v[j]);
+    crc = fold_chunks(lds, c, h);
+  } else {
+    uint32_t(*tab)[256] = lds.slice;  // the first four slicing tables
+    fill_crc_tables(tab);
+    __syncthreads();
+    crc = block_crc32(rec + kHeaderBytes, p.plan, tab, lds.seg);
+  }
   const int64_t start = static_cast<int64_t>(r) * L.block_tokens;
   const int64_t valid = p.tokens - start < L.block_tokens ? p.tokens - start : L.block_tokens;
   if (threadIdx.x < kHeaderBytes / 4) {
@@ -305,6 +504,13 @@ __global__ __launch_bounds__(kCrcThreads) void encode_header_kernel(EncodeParams
   }
   for (int64_t i = kHeaderBytes + L.payload_bytes() + threadIdx.x; i < L.record_bytes(); i += blockDim.x) rec[i] = 0;
   if (threadIdx.x == 0) p.crcs[r] = crc;
+}
+
+// the chunked CRC / gather form applies: all four arrays 16-byte multiples and
+// the payload at most kMaxRows rows of chunks
+bool chunked_layout(const Layout& L) {
+  return L.scale_bytes() % kChunkBytes == 0 && L.packed_bytes() % kChunkBytes == 0 &&
+         L.payload_bytes() <= static_cast<int64_t>(kMaxRows) * kStrideBytes;
 }
 
 int check_layout(const kvssd_record_layout* l, Layout* out) {
@@ -367,7 +573,14 @@ int launch_gather_records(const kvssd_record_layout* layout, const uint8_t* reco
   p.sv = reinterpret_cast<uint8_t*>(scales_v);
   p.valid = valid;
   p.status = status;
-  hipLaunchKernelGGL(gather_records_kernel, dim3(static_cast<unsigned>(n)), dim3(kCrcThreads), 0, stream, p);
+  const bool aligned16 = ((reinterpret_cast<uintptr_t>(packed_k) | reinterpret_cast<uintptr_t>(packed_v) |
+                           reinterpret_cast<uintptr_t>(scales_k) | reinterpret_cast<uintptr_t>(scales_v)) & 15u) == 0;
+  if (aligned16 && chunked_layout(L)) {
+    const ChunkPlan c = make_chunk_plan(p.plan.len);
+    hipLaunchKernelGGL(gather_chunked_kernel, dim3(static_cast<unsigned>(n)), dim3(kCrcThreads), 0, stream, p, c);
+  } else {
+    hipLaunchKernelGGL(gather_records_kernel, dim3(static_cast<unsigned>(n)), dim3(kCrcThreads), 0, stream, p);
+  }
   return hip_status(hipGetLastError(), "gather_records launch");
 }
 
@@ -407,6 +620,7 @@ int launch_encode_records(const kvssd_record_layout* layout, int dtype, const vo
   if (tokens < 0) return arg_error("token count must be non-negative");
   if (tokens == 0) return 0;
   if (!keys || !values || !records || !crcs) return arg_error("a required buffer pointer is NULL");
+  if (reinterpret_cast<uintptr_t>(records) % 4) return arg_error("records must be 4-byte aligned");
   EncodeParams p{};
   p.keys = keys;
   p.values = values;
@@ -435,7 +649,13 @@ int launch_encode_records(const kvssd_record_layout* layout, int dtype, const vo
       return arg_error("quantization input must be floating point");
   }
   if (int rc = hip_status(hipGetLastError(), "encode_records launch")) return rc;
-  hipLaunchKernelGGL(encode_header_kernel, dim3(static_cast<unsigned>(p.n)), dim3(kCrcThreads), 0, stream, p);
+  const uint32_t len = p.plan.len;
+  const ChunkPlan c = make_chunk_plan(len);
+  if (len % kChunkBytes == 0 && c.rows <= kMaxRows) {
+    hipLaunchKernelGGL(encode_header_kernel<true>, dim3(static_cast<unsigned>(p.n)), dim3(kCrcThreads), 0, stream, p, c);
+  } else {
+    hipLaunchKernelGGL(encode_header_kernel<false>, dim3(static_cast<unsigned>(p.n)), dim3(kCrcThreads), 0, stream, p, c);
+  }
   return hip_status(hipGetLastError(), "encode_records launch");
 }
 

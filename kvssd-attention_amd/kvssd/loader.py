@@ -5,6 +5,11 @@ small thread pool; ``depth`` reusable slots bound the bytes in flight.  Each
 yielded block owns copies of its four payload tensors, so recycling a slot can
 never corrupt a block a consumer still holds.
 
+``read_records`` is the record-native form used by the GPU pipeline: raw
+records land in the rows of a caller's buffer (the pipeline's page-locked
+staging slot) with no parsing, CRC or copies on the host; the GPU gather
+verifies them.
+
 The slots are pageable host memory even when ``pinned=True`` is passed: on
 ROCm, page-locked memory from the HIP runtime is not a valid O_DIRECT target
 (``preadv`` fails with EFAULT), and the slots are only bounce buffers anyway;
@@ -14,6 +19,7 @@ the pipeline's page-locked staging ring is what crosses PCIe.
 from __future__ import annotations
 
 from collections import deque
+from collections.abc import Sequence
 from concurrent.futures import Future, ThreadPoolExecutor
 from dataclasses import dataclass
 from queue import Queue
@@ -59,6 +65,9 @@ class AsyncBlockLoader:
         for _ in range(depth):
             raw = store.storage_backend.allocate_buffer(store.spec.record_bytes, pinned=False, device=device)
             self.free.put(_Slot(raw))
+        # O_DIRECT needs its own aligned pageable target; other backends read
+        # straight into the caller's rows
+        self._bounce = bool(store.storage_backend.probe().direct)
 
     def iter_blocks(self, layer: int, block_ids: list[int]) -> Iterator[PackedKVBlock]:
         pending: deque[tuple[_Slot, BlockEntry]] = deque()
@@ -87,6 +96,44 @@ class AsyncBlockLoader:
             if nxt is not None:
                 submit(nxt)
             yield block
+
+    def read_records(self, layer: int, block_ids: Sequence[int], destination: torch.Tensor) -> None:
+        """Raw records of ``block_ids`` into rows 0..n-1 of ``destination``
+        (a contiguous CPU uint8 tensor [>= n, record_bytes]), read on the I/O
+        threads.  No header or CRC check happens here."""
+        rb = self.store.spec.record_bytes
+        if (
+            destination.device.type != "cpu"
+            or destination.dtype != torch.uint8
+            or destination.dim() != 2
+            or destination.shape[1] != rb
+            or destination.shape[0] < len(block_ids)
+            or not destination.is_contiguous()
+        ):
+            raise ValueError(f"destination must be a contiguous CPU uint8 tensor [>= {len(block_ids)}, {rb}]")
+        entries = [self.store.entry(layer, b) for b in block_ids]
+        for entry in entries:
+            if entry.length != rb:
+                raise ValueError("record layout does not match manifest")
+
+        def work(entry: BlockEntry, row: torch.Tensor) -> None:
+            if not self._bounce:
+                self.store.read_into(entry, row)
+                return
+            slot = self.free.get()
+            try:
+                self.store.read_into(entry, slot.raw)
+                row.copy_(slot.raw[:rb])
+            finally:
+                self.free.put(slot)
+
+        futures = [self.executor.submit(work, e, destination[i]) for i, e in enumerate(entries)]
+        # every read finishes before the first error is raised, so no worker
+        # still writes into the destination afterwards
+        errors = [f.exception() for f in futures]
+        for err in errors:
+            if err is not None:
+                raise err
 
     def close(self) -> None:
         self.executor.shutdown(wait=True, cancel_futures=False)

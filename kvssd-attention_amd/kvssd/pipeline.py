@@ -1,109 +1,41 @@
-"""Selection, SSD prefetch, pinned staging and fused decode on one GPU.
+"""Selection, SSD prefetch, record-native staging and fused decode on one GPU.
 
 Reference: src/kvssd/pipeline.py:19-196.  The same public surface
 (``KVSSDPipeline(store, device, io_depth, stage_blocks, require_cuda_kernel,
 attention_backend)``, ``decode(query, layer, selector)``, context manager),
 re-planned for MI355X:
 
-* Staging uses a small ring of page-locked host slots, each laid out as the
-  five PackedBatch arrays back to back, with a matching device slot.  A chunk
-  is coalesced into its host slot with one ``torch.stack(out=...)`` per array
-  and crosses PCIe with ``hipMemcpyAsync`` (libkvssd_hip) on the transfer
-  stream: one copy for a full chunk instead of one ``.to()`` per tensor, and no
-  page-locked allocation per chunk (the reference pins fresh tensors for every
-  chunk, pipeline.py:98-109).
-* HIP events order the streams: the compute stream waits for a slot's copy;
-  the transfer stream waits for the kernel that last read the slot's device
-  memory before overwriting it; the host waits for a slot's previous copy only
-  before refilling that host slot.
+* The streamed path moves records, not parsed blocks: the loader's I/O
+  threads read a chunk's raw records straight into a page-locked staging slot,
+  one ``hipMemcpyAsync`` per chunk carries them to the device on the transfer
+  stream, and on the compute stream the GPU gather checks every header and
+  payload CRC-32 and lays out the PackedBatch arrays for the fused decode
+  (``kvssd.staging``).  The host never parses, checksums, clones or stacks a
+  block (the reference does all four, loader.py:73-91, pipeline.py:98-109).
 * Each chunk's (O, LSE) folds into a running accumulator with one HIP merge
   kernel (the reference issues about six torch launches, pipeline.py:147-153).
-* ``load_resident`` keeps whole layers in HBM (288 GB per MI355X); ``decode``
-  of a resident layer turns the selection into a device block table and runs a
-  single fused call with no SSD or PCIe traffic.
+* Two resident tiers sit above the SSD: ``load_host_resident`` keeps a layer's
+  raw records in page-locked host memory, so a decode of it only streams
+  PCIe; ``load_resident`` keeps the gathered PackedBatch of a layer in HBM
+  (288 GB per MI355X), and a decode of it is a single fused call over a device
+  block table with no SSD or PCIe traffic.
 """
 
 from __future__ import annotations
 
-import ctypes
 import math
-from collections.abc import Iterator, Sequence
+from collections.abc import Sequence
 from dataclasses import dataclass
 
 import torch
 
-from . import _native
-from .attention import merge_attention_chunks, packed_attention, resolve_required
+from .attention import packed_attention, resolve_required
 from .backends import AttentionBackend, PackedBatch
-from .format import CacheSpec, PackedKVBlock
 from .loader import AsyncBlockLoader
+from .records_hip import gather_records, raise_for_status
 from .selectors import AllBlocks, BlockSelector
+from .staging import HostRecords, RecordStager
 from .store import KVCacheStore
-
-_STAGING_SLOTS = 3
-_ALIGN = 256
-
-
-def _aligned(n: int) -> int:
-    return -(-n // _ALIGN) * _ALIGN
-
-
-@dataclass
-class _Layout:
-    """Byte offsets of the five PackedBatch arrays inside one staging slot."""
-
-    capacity: int
-    packed: int  # bytes per block of one packed array
-    scales: int  # bytes per block of one scale array
-    off_kp: int
-    off_vp: int
-    off_ks: int
-    off_vs: int
-    off_valid: int
-    total: int
-
-    @classmethod
-    def for_spec(cls, spec: CacheSpec, capacity: int) -> "_Layout":
-        packed = spec.block_tokens * spec.kv_heads * spec.packed_dim
-        scales = spec.block_tokens * spec.kv_heads * (spec.head_dim // spec.group_size) * 2
-        off_kp = 0
-        off_vp = off_kp + _aligned(capacity * packed)
-        off_ks = off_vp + _aligned(capacity * packed)
-        off_vs = off_ks + _aligned(capacity * scales)
-        off_valid = off_vs + _aligned(capacity * scales)
-        total = off_valid + _aligned(capacity * 4)
-        return cls(capacity, packed, scales, off_kp, off_vp, off_ks, off_vs, off_valid, total)
-
-    def views(self, buf: torch.Tensor, spec: CacheSpec, n: int) -> tuple[torch.Tensor, ...]:
-        groups = spec.head_dim // spec.group_size
-        pshape = (n, spec.block_tokens, spec.kv_heads, spec.packed_dim)
-        sshape = (n, spec.block_tokens, spec.kv_heads, groups)
-        kp = buf[self.off_kp : self.off_kp + n * self.packed].view(pshape)
-        vp = buf[self.off_vp : self.off_vp + n * self.packed].view(pshape)
-        ks = buf[self.off_ks : self.off_ks + n * self.scales].view(torch.float16).view(sshape)
-        vs = buf[self.off_vs : self.off_vs + n * self.scales].view(torch.float16).view(sshape)
-        valid = buf[self.off_valid : self.off_valid + 4 * n].view(torch.int32)
-        return kp, vp, ks, vs, valid
-
-    def spans(self, n: int) -> list[tuple[int, int]]:
-        """(offset, bytes) ranges holding a chunk of n blocks; one range when full."""
-        if n == self.capacity:
-            return [(0, self.off_valid + 4 * n)]
-        return [
-            (self.off_kp, n * self.packed),
-            (self.off_vp, n * self.packed),
-            (self.off_ks, n * self.scales),
-            (self.off_vs, n * self.scales),
-            (self.off_valid, 4 * n),
-        ]
-
-
-class _Slot:
-    def __init__(self, layout: _Layout, device: torch.device):
-        self.host = torch.empty(layout.total, dtype=torch.uint8, pin_memory=True)
-        self.dev = torch.empty(layout.total, dtype=torch.uint8, device=device)
-        self.copied: torch.cuda.Event | None = None  # H2D from this slot finished
-        self.consumed: torch.cuda.Event | None = None  # kernel reading self.dev finished
 
 
 @dataclass
@@ -136,118 +68,75 @@ class KVSSDPipeline:
         self.attention_backend = resolve_required(require_cuda_kernel, attention_backend, self.device)
         gpu = self.device.type == "cuda"
         self.transfer_stream = torch.cuda.Stream(device=self.device) if gpu else None
+        # a second copy stream: successive chunks alternate between the two
+        self._transfer_alt = torch.cuda.Stream(device=self.device) if gpu else None
         self.compute_stream = torch.cuda.Stream(device=self.device) if gpu else None
-        self._layout: _Layout | None = None
-        self._slots: list[_Slot] = []
+        self._stager: RecordStager | None = None
         self._resident: dict[int, _Resident] = {}
+        self._host: dict[int, HostRecords] = {}
 
     # ------------------------------------------------------------ helpers ---
-    @staticmethod
-    def _chunks(source: Iterator[PackedKVBlock], size: int) -> Iterator[list[PackedKVBlock]]:
-        chunk: list[PackedKVBlock] = []
-        for block in source:
-            chunk.append(block)
-            if len(chunk) == size:
-                yield chunk
-                chunk = []
-        if chunk:
-            yield chunk
+    def _require_gpu(self, what: str) -> None:
+        if self.device.type != "cuda":
+            raise RuntimeError(f"{what} need a GPU device")
 
-    def _ensure_slots(self) -> None:
-        if self._slots:
-            return
-        self._layout = _Layout.for_spec(self.store.spec, self.stage_blocks)
-        self._slots = [_Slot(self._layout, self.device) for _ in range(_STAGING_SLOTS)]
+    def _staging(self) -> RecordStager:
+        if self._stager is None:
+            assert self.transfer_stream is not None and self.compute_stream is not None
+            self._stager = RecordStager(
+                self.store.spec,
+                self.device,
+                self.stage_blocks,
+                self.attention_backend,
+                [self.transfer_stream, self._transfer_alt],
+                self.compute_stream,
+            )
+        return self._stager
 
-    def _stage(self, blocks: Sequence[PackedKVBlock], slot: _Slot) -> tuple[tuple[torch.Tensor, ...], torch.cuda.Event]:
-        """Coalesce a chunk into a pinned slot and enqueue its H2D copy on the transfer stream."""
-        assert self.transfer_stream is not None and self._layout is not None
-        spec, layout, n = self.store.spec, self._layout, len(blocks)
-        if slot.copied is not None:
-            slot.copied.synchronize()  # the host slot is still being read by a previous copy
-        kp, vp, ks, vs, valid = layout.views(slot.host, spec, n)
-        torch.stack([b.key.packed for b in blocks], out=kp)
-        torch.stack([b.value.packed for b in blocks], out=vp)
-        torch.stack([b.key.scales for b in blocks], out=ks)
-        torch.stack([b.value.scales for b in blocks], out=vs)
-        valid.copy_(torch.tensor([b.valid_tokens for b in blocks], dtype=torch.int32))
-        lib = _native.load()
-        stream = _native.stream_handle(self.transfer_stream)
-        if slot.consumed is not None:
-            self.transfer_stream.wait_event(slot.consumed)
-        host, dev = slot.host.data_ptr(), slot.dev.data_ptr()
-        for off, nbytes in layout.spans(n):
-            rc = lib.kvssd_hip_memcpy_h2d_async(ctypes.c_void_p(dev + off), ctypes.c_void_p(host + off), nbytes, stream)
-            _native.check(rc, "kvssd_hip_memcpy_h2d_async")
-        copied = torch.cuda.Event()
-        copied.record(self.transfer_stream)
-        slot.copied = copied
-        return layout.views(slot.dev, spec, n), copied
-
-    def _merge(self, acc: tuple[torch.Tensor, torch.Tensor] | None, out: torch.Tensor, lse: torch.Tensor):
-        if acc is None:
-            return out, lse
-        merge = getattr(self.attention_backend, "merge_chunks", None)
-        if merge is not None:
-            merge(acc[0], acc[1], out, lse)
-            return acc
-        return merge_attention_chunks(acc[0], acc[1], out, lse)
+    def _read_layer(self, layer: int) -> HostRecords:
+        ids = self.store.blocks_for_layer(layer)
+        if not ids:
+            raise ValueError(f"layer {layer} has no blocks")
+        records = torch.empty((len(ids), self.store.spec.record_bytes), dtype=torch.uint8, pin_memory=True)
+        self.loader.read_records(layer, ids, records)
+        return HostRecords(records, ids)
 
     # ---------------------------------------------------------- streamed ---
     def _decode_streamed(self, query: torch.Tensor, layer: int, selected: list[int]) -> torch.Tensor:
-        assert self.compute_stream is not None and self.transfer_stream is not None
-        self._ensure_slots()
-        chunks = self._chunks(self.loader.iter_blocks(layer, selected), self.stage_blocks)
-        first = next(chunks, None)
-        if first is None:
-            raise ValueError("selector returned no blocks")
-        spec = self.store.spec
-        scale = 1.0 / math.sqrt(query.shape[-1])
-        caller = torch.cuda.current_stream(self.device)
-        self.compute_stream.wait_stream(caller)
-        query.record_stream(self.compute_stream)
-        acc: tuple[torch.Tensor, torch.Tensor] | None = None
-        index = 0
-        current = self._stage(first, self._slots[0])
-        while current is not None:
-            slot = self._slots[index % len(self._slots)]
-            tensors, ready = current
-            with torch.cuda.stream(self.compute_stream):
-                self.compute_stream.wait_event(ready)
-                out, lse = self.attention_backend.run(query, PackedBatch(*tensors, spec.bits, spec.group_size), scale)
-                acc = self._merge(acc, out, lse)
-                consumed = torch.cuda.Event()
-                consumed.record(self.compute_stream)
-                slot.consumed = consumed
-            # read + stage the next chunk while the kernel runs
-            nxt = next(chunks, None)
-            index += 1
-            current = None if nxt is None else self._stage(nxt, self._slots[index % len(self._slots)])
-        assert acc is not None
-        done = torch.cuda.Event()
-        done.record(self.compute_stream)
-        caller.wait_event(done)
-        acc[0].record_stream(caller)
-        return acc[0].to(query.dtype)
+        stager = self._staging()
+        host = self._host.get(layer)
+        if host is not None:
+            fill = stager.host_fill(host)
+        else:
+            fill = stager.read_fill(lambda ids, rows: self.loader.read_records(layer, ids, rows))
+        out, _ = stager.run(query, 1.0 / math.sqrt(query.shape[-1]), layer, selected, fill)
+        return out.to(query.dtype)
 
     # ---------------------------------------------------------- resident ---
+    def load_host_resident(self, layers: Sequence[int] | None = None) -> None:
+        """Keep whole layers' raw records in page-locked host memory; later
+        decodes of them stream PCIe only (records are still CRC-checked on the GPU)."""
+        self._require_gpu("host-resident layers")
+        for layer in layers if layers is not None else range(self.store.spec.layers):
+            self._host[layer] = self._read_layer(layer)
+
+    def release_host_resident(self, layers: Sequence[int] | None = None) -> None:
+        for layer in list(self._host) if layers is None else layers:
+            self._host.pop(layer, None)
+
     def load_resident(self, layers: Sequence[int] | None = None) -> None:
-        """Copy whole layers into device memory; later decodes of them read HBM only."""
-        if self.device.type != "cuda":
-            raise RuntimeError("resident layers need a GPU device")
+        """Copy whole layers into device memory; later decodes of them read HBM only.
+        The records cross PCIe once and are checked and gathered on the GPU."""
+        self._require_gpu("resident layers")
         spec = self.store.spec
         for layer in layers if layers is not None else range(spec.layers):
-            ids = self.store.blocks_for_layer(layer)
-            if not ids:
-                raise ValueError(f"layer {layer} has no blocks")
-            blocks = list(self.loader.iter_blocks(layer, ids))
-            kp = torch.stack([b.key.packed for b in blocks]).to(self.device)
-            vp = torch.stack([b.value.packed for b in blocks]).to(self.device)
-            ks = torch.stack([b.key.scales for b in blocks]).to(self.device)
-            vs = torch.stack([b.value.scales for b in blocks]).to(self.device)
-            valid = torch.tensor([b.valid_tokens for b in blocks], dtype=torch.int32, device=self.device)
+            host = self._host.get(layer) or self._read_layer(layer)
+            raw = host.records.view(-1).to(self.device)
+            kp, vp, ks, vs, valid, status = gather_records(raw, spec, len(host.block_ids))
+            raise_for_status(status, layer, host.block_ids)
+            del raw
             batch = PackedBatch(kp, vp, ks, vs, valid, spec.bits, spec.group_size)
-            self._resident[layer] = _Resident(batch, {bid: row for row, bid in enumerate(ids)})
+            self._resident[layer] = _Resident(batch, dict(host.row_of))
 
     def release_resident(self, layers: Sequence[int] | None = None) -> None:
         for layer in list(self._resident) if layers is None else layers:
@@ -283,7 +172,7 @@ class KVSSDPipeline:
         query = query.to(self.device)
         if layer in self._resident:
             return self._decode_resident(query, layer, selected)
-        if self.device.type == "cuda" and self.attention_backend.probe(self.device).accelerated:
+        if self.device.type == "cuda" and (layer in self._host or self.attention_backend.probe(self.device).accelerated):
             return self._decode_streamed(query, layer, selected)
         blocks = list(self.loader.iter_blocks(layer, selected))
         return packed_attention(
@@ -297,6 +186,7 @@ class KVSSDPipeline:
     def close(self) -> None:
         self.loader.close()
         self._resident.clear()
+        self._host.clear()
 
     def __enter__(self) -> "KVSSDPipeline":
         return self

@@ -44,26 +44,55 @@ def record_bytes(spec: CacheSpec) -> int:
     return int(out.value)
 
 
+def _check_out(out: tuple[torch.Tensor, ...], spec: CacheSpec, count: int, dev: torch.device) -> None:
+    groups = spec.head_dim // spec.group_size
+    pshape = (count, spec.block_tokens, spec.kv_heads, spec.packed_dim)
+    sshape = (count, spec.block_tokens, spec.kv_heads, groups)
+    want = [
+        (pshape, torch.uint8),
+        (pshape, torch.uint8),
+        (sshape, torch.float16),
+        (sshape, torch.float16),
+        ((count,), torch.int32),
+        ((count,), torch.int32),
+    ]
+    if len(out) != len(want):
+        raise ValueError("out must hold (packed_k, packed_v, scales_k, scales_v, valid, status)")
+    for t, (shape, dtype) in zip(out, want):
+        if tuple(t.shape) != shape or t.dtype != dtype or t.device != dev or not t.is_contiguous():
+            raise ValueError(f"gather output must be a contiguous {dtype} tensor of shape {shape} on {dev}")
+
+
 def gather_records(
-    raw: torch.Tensor, spec: CacheSpec, count: int, stride: int | None = None, verify_crc: bool = True
+    raw: torch.Tensor,
+    spec: CacheSpec,
+    count: int,
+    stride: int | None = None,
+    verify_crc: bool = True,
+    out: tuple[torch.Tensor, ...] | None = None,
 ) -> tuple[torch.Tensor, ...]:
     """(packed_k, packed_v, scales_k, scales_v, valid, status) of ``count``
     records held back to back (``stride`` bytes apart, default
     ``record_bytes``) in the device uint8 tensor ``raw``.  ``status`` holds
-    per record OK, BAD_HEADER, BAD_LAYOUT or BAD_CRC; see :func:`raise_for_status`."""
+    per record OK, BAD_HEADER, BAD_LAYOUT or BAD_CRC; see :func:`raise_for_status`.
+    ``out`` supplies the six output tensors (else they are allocated)."""
     stride = spec.record_bytes if stride is None else stride
     if raw.dtype != torch.uint8 or raw.device.type != "cuda" or not raw.is_contiguous():
         raise TypeError("raw records must be a contiguous uint8 device tensor")
     if raw.numel() < count * stride:
         raise ValueError("raw buffer holds fewer than count records")
     dev = raw.device
-    bt, kvh = spec.block_tokens, spec.kv_heads
-    pk = torch.empty((count, bt, kvh, spec.packed_dim), dtype=torch.uint8, device=dev)
-    pv = torch.empty_like(pk)
-    sk = torch.empty((count, bt, kvh, spec.head_dim // spec.group_size), dtype=torch.float16, device=dev)
-    sv = torch.empty_like(sk)
-    valid = torch.empty(count, dtype=torch.int32, device=dev)
-    status = torch.empty(count, dtype=torch.int32, device=dev)
+    if out is not None:
+        _check_out(out, spec, count, dev)
+        pk, pv, sk, sv, valid, status = out
+    else:
+        bt, kvh = spec.block_tokens, spec.kv_heads
+        pk = torch.empty((count, bt, kvh, spec.packed_dim), dtype=torch.uint8, device=dev)
+        pv = torch.empty_like(pk)
+        sk = torch.empty((count, bt, kvh, spec.head_dim // spec.group_size), dtype=torch.float16, device=dev)
+        sv = torch.empty_like(sk)
+        valid = torch.empty(count, dtype=torch.int32, device=dev)
+        status = torch.empty(count, dtype=torch.int32, device=dev)
     rc = _native.load().kvssd_hip_gather_records(
         ctypes.byref(_layout(spec)),
         raw.data_ptr(),

@@ -125,3 +125,92 @@ def test_sparse_selection_262k_tokens(cuda_device):
         out, lse = HipAttentionBackend(kernel).run(q.to(dev), batch, scale, block_table=ids)
         np.testing.assert_allclose(out.cpu().numpy(), ref_out, atol=ATOL, rtol=RTOL)
         np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("stage_blocks", [2, 5])
+def test_host_resident_layer_matches_oracle(cuda_device, tmp_path: Path, stage_blocks: int):
+    # raw records kept in page-locked host memory: chunks cross PCIe in runs of
+    # consecutive records and are gathered + CRC-checked on the GPU
+    store, (pk, pv, sk, sv, valid) = build_store(tmp_path, 2500, 4)
+    query = torch.randn(32, 128, generator=torch.Generator().manual_seed(4), dtype=torch.float16)
+    scale = 1 / math.sqrt(128)
+    with KVSSDPipeline(store, device=cuda_device, stage_blocks=stage_blocks, attention_backend="hip") as pipe:
+        pipe.load_host_resident([0])
+        for selector in (AllBlocks(), RecentSinkBlocks(3, 6), RecentSinkBlocks(1, 0)):
+            out = pipe.decode(query, 0, selector)
+            ids = np.array(selector.select(list(range(20))), np.int32)
+            ref, _ = O.attention(query.float().numpy(), pk, pv, sk, sv, valid, 4, 32, scale, block_table=ids)
+            np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+        # HBM residency built from the host tier gives the same answer
+        pipe.load_resident([0])
+        out = pipe.decode(query, 0, RecentSinkBlocks(3, 6))
+        ids = np.array(RecentSinkBlocks(3, 6).select(list(range(20))), np.int32)
+        ref, _ = O.attention(query.float().numpy(), pk, pv, sk, sv, valid, 4, 32, scale, block_table=ids)
+        np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+
+
+def corrupt(path: Path, store: KVCacheStore, block: int, at: int, value: bytes) -> None:
+    e = store.entry(0, block)
+    with (path / "blocks.kvssd").open("r+b") as f:
+        f.seek(e.offset + at)
+        f.write(value)
+
+
+def test_streamed_decode_raises_on_corrupt_records(cuda_device, tmp_path: Path):
+    # a flipped payload byte raises decode_record's IOError from the GPU CRC
+    # check; a bad magic raises its ValueError; unselected blocks are not read
+    store, _ = build_store(tmp_path, 1024, 4)  # 8 blocks
+    query = torch.randn(32, 128, dtype=torch.float16)
+    corrupt(tmp_path, store, 5, 52 + 20000, b"\x5a")
+    with KVSSDPipeline(store, device=cuda_device, stage_blocks=3, attention_backend="hip") as pipe:
+        with pytest.raises(IOError, match="CRC mismatch for layer=0, block=5"):
+            pipe.decode(query, 0)
+        assert torch.isfinite(pipe.decode(query, 0, RecentSinkBlocks(2, 1))).all()
+        with pytest.raises(IOError, match="block=5"):
+            pipe.load_resident([0])
+        pipe.load_host_resident([0])
+        with pytest.raises(IOError, match="block=5"):
+            pipe.decode(query, 0, RecentSinkBlocks(0, 3))
+    corrupt(tmp_path, store, 1, 0, b"KVSSD999")
+    with KVSSDPipeline(store, device=cuda_device, stage_blocks=4, attention_backend="hip") as pipe:
+        with pytest.raises(ValueError, match="invalid KVSSD record header"):
+            pipe.decode(query, 0, RecentSinkBlocks(2, 0))
+
+
+def test_host_staged_1m_tokens(cuda_device):
+    # the 1,048,576-token host-staged workload: raw records of the layer in
+    # page-locked host memory, streamed in 64-record chunks (one H2D each),
+    # gathered, CRC-checked, decoded and merged on the GPU; parity with the
+    # oracle over the same records parsed on the host
+    from kvssd import records_hip as R
+    from kvssd.staging import HostRecords, RecordStager
+
+    spec = CacheSpec(1, 8, 128, 128, 4, 32)
+    nb, dev = 8192, cuda_device
+    gen = torch.Generator(device=dev).manual_seed(13)
+    keys = torch.randn(nb * 128, 8, 128, generator=gen, device=dev, dtype=torch.float16)
+    values = torch.randn(nb * 128, 8, 128, generator=gen, device=dev, dtype=torch.float16)
+    query = torch.randn(32, 128, generator=gen, device=dev, dtype=torch.float16)
+    records, _ = R.encode_records(keys, values, spec, layer=0)
+    del keys, values
+    pinned = torch.empty(records.shape, dtype=torch.uint8, pin_memory=True)
+    pinned.copy_(records)
+    del records
+    scale = 1 / math.sqrt(128)
+    backend = HipAttentionBackend()
+    stager = RecordStager(spec, dev, 64, backend, torch.cuda.Stream(dev), torch.cuda.Stream(dev))
+    ids = list(range(nb))
+    out, lse = stager.run(query, scale, 0, ids, stager.host_fill(HostRecords(pinned, ids)))
+    torch.cuda.synchronize()
+
+    raw = pinned.numpy()
+    s, pb = 128 * 8 * 4 * 2, 128 * 8 * 64
+    base = 52
+    sk = np.ascontiguousarray(raw[:, base : base + s]).view(np.float16).reshape(nb, 128, 8, 4)
+    sv = np.ascontiguousarray(raw[:, base + s : base + 2 * s]).view(np.float16).reshape(nb, 128, 8, 4)
+    pk = np.ascontiguousarray(raw[:, base + 2 * s : base + 2 * s + pb]).reshape(nb, 128, 8, 64)
+    pv = np.ascontiguousarray(raw[:, base + 2 * s + pb : base + 2 * s + 2 * pb]).reshape(nb, 128, 8, 64)
+    valid = np.full(nb, 128, np.int32)
+    ref_out, ref_lse = O.attention(query.float().cpu().numpy(), pk, pv, sk, sv, valid, 4, 32, scale, threads=16)
+    np.testing.assert_allclose(out.cpu().numpy(), ref_out, atol=ATOL, rtol=RTOL)
+    np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=ATOL, rtol=RTOL)

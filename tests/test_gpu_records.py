@@ -99,6 +99,10 @@ SPECS = [
     CacheSpec(layers=1, kv_heads=2, head_dim=64, block_tokens=32, bits=4, group_size=16),
     # payload of 6 * BT * KVH = 18 bytes: not a multiple of 4 (byte paths)
     CacheSpec(layers=1, kv_heads=1, head_dim=4, block_tokens=3, bits=2, group_size=4),
+    # 55,296-byte payload: 4 rows of 16-byte chunks behind 10,240 virtual zero bytes
+    CacheSpec(layers=1, kv_heads=8, head_dim=128, block_tokens=48, bits=4, group_size=32),
+    # 294,912-byte payload: beyond the chunked form's 256 KiB, general form
+    CacheSpec(layers=1, kv_heads=8, head_dim=128, block_tokens=256, bits=4, group_size=32),
 ]
 
 
@@ -182,3 +186,27 @@ def test_gather_then_decode_matches_oracle(cuda_device):
     ref_out, ref_lse = O.attention(q, opk, opv, osk, osv, ovalid, 4, 32, 0.1)
     np.testing.assert_allclose(out.cpu().numpy(), ref_out, atol=2e-3, rtol=1e-2)
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=2e-3, rtol=1e-2)
+
+
+def test_gather_records_unaligned_outputs(cuda_device):
+    # outputs that are not 16-byte aligned take the general form; same bytes
+    spec = SPECS[0]
+    rng = np.random.default_rng(6)
+    k = rng.standard_normal((3 * spec.block_tokens, spec.kv_heads, spec.head_dim)).astype(np.float32)
+    recs = oracle_records(k, k[::-1].copy(), spec, 0, 0)
+    raw = device_records(recs, cuda_device)
+    want = R.gather_records(raw, spec, 3)
+    n, bt, kvh = 3, spec.block_tokens, spec.kv_heads
+    pbytes = n * bt * kvh * spec.packed_dim
+    sbytes = n * bt * kvh * (spec.head_dim // spec.group_size) * 2
+    buf = torch.zeros(2 * pbytes + 2 * sbytes + 64, dtype=torch.uint8, device=cuda_device)
+    pk = buf[4 : 4 + pbytes].view(n, bt, kvh, spec.packed_dim)
+    pv = buf[8 + pbytes : 8 + 2 * pbytes].view(n, bt, kvh, spec.packed_dim)
+    base = 16 + 2 * pbytes
+    sk = buf[base : base + sbytes].view(torch.float16).view(n, bt, kvh, -1)
+    sv = buf[base + sbytes + 8 : base + 2 * sbytes + 8].view(torch.float16).view(n, bt, kvh, -1)
+    valid = torch.empty(n, dtype=torch.int32, device=cuda_device)
+    status = torch.empty(n, dtype=torch.int32, device=cuda_device)
+    got = R.gather_records(raw, spec, n, out=(pk, pv, sk, sv, valid, status))
+    for a, b in zip(got, want):
+        assert torch.equal(a.view(torch.uint8) if a.dtype == torch.float16 else a, b.view(torch.uint8) if b.dtype == torch.float16 else b)

@@ -110,3 +110,39 @@ def test_storage_backends_fail_closed(tmp_path: Path) -> None:
     with pytest.raises(ValueError, match="unknown storage backend"):
         resolve_storage_backend("nvme-of", tmp_path / "blocks.kvssd")
     assert resolve_storage_backend("buffered", tmp_path / "blocks.kvssd").name == "buffered"
+
+
+@pytest.mark.parametrize("storage", ["buffered", "direct"])
+def test_read_records_copies_raw_bytes_in_order(tmp_path: Path, storage: str) -> None:
+    # the record-native read: rows hold the file's record bytes, in the order asked
+    store, _, _ = make_store(tmp_path, storage=storage)
+    rb = store.spec.record_bytes
+    raw = (tmp_path / "blocks.kvssd").read_bytes()
+    ids = [2, 0, 1]
+    dest = torch.zeros((4, rb), dtype=torch.uint8)
+    with AsyncBlockLoader(store, depth=2) as loader:
+        loader.read_records(1, ids, dest)
+        for row, b in enumerate(ids):
+            e = store.entry(1, b)
+            assert dest[row].numpy().tobytes() == raw[e.offset : e.offset + e.length]
+        assert int(dest[3].count_nonzero()) == 0
+        with pytest.raises(ValueError, match="destination"):
+            loader.read_records(1, ids, torch.zeros((2, rb), dtype=torch.uint8))
+        with pytest.raises(KeyError):
+            loader.read_records(1, [7], dest)
+
+
+def test_host_records_spans_follow_runs() -> None:
+    # one H2D span per run of consecutive rows, destination offsets in id order
+    from kvssd.staging import HostRecords
+
+    recs = torch.zeros((10, 4096), dtype=torch.uint8)
+    host = HostRecords(recs, list(range(100, 110)))
+    base = recs.data_ptr()
+    spans = host.spans([100, 101, 102, 105, 106, 109, 103], 4096)
+    assert spans == [
+        (base, 0, 3 * 4096),
+        (base + 5 * 4096, 3 * 4096, 2 * 4096),
+        (base + 9 * 4096, 5 * 4096, 4096),
+        (base + 3 * 4096, 6 * 4096, 4096),
+    ]
