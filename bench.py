@@ -57,6 +57,11 @@ WORKLOADS = {
 HOST_STAGED = {
     "int4_gqa_1m_host_staged": (1048576, 4, 32, 64),
 }
+# name -> (kernel, tokens, bits): the record codec on one layer held in HBM
+CODEC = {
+    "gather_int4_128k": ("gather", 131072, 4),
+    "encode_int4_128k": ("encode", 131072, 4),
+}
 KV_HEADS, HEAD_DIM, BLOCK_TOKENS, GROUP = 8, 128, 128, 32
 
 
@@ -142,6 +147,86 @@ def copy_calibration(torch, dev, nbytes: int, steps: int, warmup: int) -> int:
     ms = start.elapsed_time(end) / steps
     print(json.dumps({"copy_bytes": nbytes, "steps": steps, "ms_per_copy": round(ms, 5),
                       "read_GBps": round(nbytes / ms / 1e6, 1)}), flush=True)
+    return 0
+
+
+def codec(torch, dev, args) -> int:
+    """One launch of the record gather (records -> PackedBatch arrays with the
+    CRC check) or of the record encoder (fp16 K/V -> records) over one layer
+    in HBM; several copies rotate so the Infinity Cache cannot serve repeats."""
+    from kvssd.format import CacheSpec
+    from kvssd.records_hip import encode_records, gather_records
+
+    kind, tokens, bits = CODEC[args.workload]
+    spec = CacheSpec(1, KV_HEADS, HEAD_DIM, BLOCK_TOKENS, bits, GROUP)
+    nb = tokens // BLOCK_TOKENS
+    gen = torch.Generator(device=dev).manual_seed(7)
+    keys = torch.randn(tokens, KV_HEADS, HEAD_DIM, generator=gen, device=dev, dtype=torch.float16)
+    values = torch.randn(tokens, KV_HEADS, HEAD_DIM, generator=gen, device=dev, dtype=torch.float16)
+    records, crcs = encode_records(keys, values, spec, layer=0)
+    payload = spec.payload_bytes
+    copies = args.copies or 4
+    if kind == "gather":
+        raws = [records.view(-1)] + [records.view(-1).clone() for _ in range(copies - 1)]
+        outs = [gather_records(r, spec, nb) for r in raws]
+
+        def launch(i):
+            r = raws[i % copies]
+            gather_records(r, spec, nb, out=outs[i % copies])
+
+        # header + payload read, four arrays + valid + status written
+        nbytes = nb * ((52 + payload) + payload + 8)
+        name = "gather_chunked_kernel"
+    else:
+        ins = [(keys, values)] + [(keys.clone(), values.clone()) for _ in range(copies - 1)]
+
+        def launch(i):
+            k, v = ins[i % copies]
+            encode_records(k, v, spec, 0)  # allocates its outputs; timed with them
+
+        # fp16 K and V read, whole records written
+        nbytes = 2 * tokens * KV_HEADS * HEAD_DIM * 2 + nb * spec.record_bytes
+        name = "encode_payload_kernel + encode_header_kernel"
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        evs[i][0].record(stream)
+        launch(i)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) for a, b in evs)
+    med = ms[len(ms) // 2]
+    # the gathered arrays / encoded records are checked against each other once
+    ok = True
+    if kind == "gather":
+        pk, pv, sk, sv, valid, status = outs[0]
+        ok = int(status.max()) == 0 and int(valid.min()) == BLOCK_TOKENS
+    else:
+        again, crc2 = encode_records(keys, values, spec, 0)
+        ok = bool(torch.equal(again, records)) and bool(torch.equal(crc2, crcs))
+    gbps = nbytes / (med * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": f"record {kind} GB/s (algorithmic bytes), INT4 128K tokens",
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(med, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8" if kind == "gather" else "f16",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "tokens": tokens, "bits": bits, "records": nb,
+                   "record_bytes": spec.record_bytes, "alg_bytes_per_step": nbytes, "copies_rotated": copies},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": name},
+        "ok": ok,
+    }), flush=True)
     return 0
 
 
@@ -285,7 +370,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="int4_gqa_128k", choices=sorted(WORKLOADS) + sorted(HOST_STAGED))
+    ap.add_argument("--workload", default="int4_gqa_128k", choices=sorted(WORKLOADS) + sorted(HOST_STAGED) + sorted(CODEC))
     ap.add_argument("--kernel", default="auto", choices=["auto", "general", "mfma", "staged", "pairs"])
     ap.add_argument("--copies", type=int, default=0, help="distinct KV copies rotated across steps (0 = auto)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -318,6 +403,8 @@ def main() -> int:
         return copy_calibration(torch, dev, args.copy_calibration, args.steps, args.warmup)
     if args.workload in HOST_STAGED:
         return host_staged(torch, dev, args)
+    if args.workload in CODEC:
+        return codec(torch, dev, args)
     tokens, bits, qh, vscale, outl, sel = WORKLOADS[args.workload]
     query, cache, valid = make_cache(torch, dev, tokens, bits, qh, vscale, outl)
     nb = tokens // BLOCK_TOKENS

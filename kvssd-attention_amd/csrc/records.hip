@@ -402,12 +402,53 @@ __device__ __forceinline__ void quantize_group(const T* src, int group_size, int
   *scale = __builtin_bit_cast(uint16_t, static_cast<_Float16>(s32));
 }
 
-template <typename T>
+// The same arithmetic for a 32-value group held in registers: the group is
+// read once with wide loads (src 16-byte aligned) and its packed bytes go out
+// in one 4-byte aligned store of 4 (INT4) or 2 (INT2) words.
+constexpr int kRegGroup = 32;
+
+template <typename T, int BITS>
+__device__ __forceinline__ void quantize_group_reg(const T* src, uint8_t* packed, uint16_t* scale) {
+  float x[kRegGroup];
+  if (src) {
+    T v[kRegGroup];
+    __builtin_memcpy(v, __builtin_assume_aligned(src, 16), sizeof(v));
+#pragma unroll
+    for (int i = 0; i < kRegGroup; ++i) x[i] = to_f32(v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kRegGroup; ++i) x[i] = 0.0f;
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kRegGroup; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  constexpr int mid = 1 << (BITS - 1);
+  const float s32 = fmaxf(amax, 1e-8f) / static_cast<float>(mid - 1);
+  constexpr int words = kRegGroup * BITS / 32;
+  uint32_t w[words];
+#pragma unroll
+  for (int k = 0; k < words; ++k) w[k] = 0;
+#pragma unroll
+  for (int i = 0; i < kRegGroup; ++i) {
+    const float c = fminf(fmaxf(rintf(x[i] / s32), static_cast<float>(-mid)), static_cast<float>(mid - 1));
+    w[(i * BITS) >> 5] |= static_cast<uint32_t>(static_cast<int>(c) + mid) << ((i * BITS) & 31);
+  }
+  __builtin_memcpy(__builtin_assume_aligned(packed, 4), w, sizeof(w));
+  *scale = __builtin_bit_cast(uint16_t, static_cast<_Float16>(s32));
+}
+
+// BITS == 0: any group size (quantize_group); BITS == 2 / 4: group_size 32
+// in registers (quantize_group_reg)
+template <typename T, int BITS>
 __global__ __launch_bounds__(256) void quantize_kernel(const T* __restrict__ x, int64_t groups, int group_size, int bits,
                                                        uint8_t* __restrict__ packed, uint16_t* __restrict__ scales) {
   const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (g >= groups) return;
-  quantize_group(x + g * group_size, group_size, bits, packed + g * (group_size * bits / 8), scales + g);
+  if constexpr (BITS == 0) {
+    quantize_group(x + g * group_size, group_size, bits, packed + g * (group_size * bits / 8), scales + g);
+  } else {
+    quantize_group_reg<T, BITS>(x + g * kRegGroup, packed + g * (kRegGroup * BITS / 8), scales + g);
+  }
 }
 
 // ------------------------------------------------------------------ encode ---
@@ -423,8 +464,9 @@ struct EncodeParams {
 };
 
 // phase 1: every (record, key/value, token, kv head, group) quantised into
-// the record's payload; tokens past the end read as zeros
-template <typename T>
+// the record's payload; tokens past the end read as zeros.  BITS as in
+// quantize_kernel.
+template <typename T, int BITS>
 __global__ __launch_bounds__(256) void encode_payload_kernel(EncodeParams p) {
   const Layout& L = p.lay;
   const int G = L.head_dim / L.group_size;
@@ -445,7 +487,11 @@ __global__ __launch_bounds__(256) void encode_payload_kernel(EncodeParams p) {
   const int64_t s = L.scale_bytes(), pb = L.packed_bytes();
   uint16_t* scale = reinterpret_cast<uint16_t*>(pay + (is_v ? s : 0)) + q;
   uint8_t* packed = pay + 2 * s + (is_v ? pb : 0) + q * (L.group_size * L.bits / 8);
-  quantize_group(src, L.group_size, L.bits, packed, scale);
+  if constexpr (BITS == 0) {
+    quantize_group(src, L.group_size, L.bits, packed, scale);
+  } else {
+    quantize_group_reg<T, BITS>(src, packed, scale);
+  }
 }
 
 // phase 2: one workgroup per record -- CRC of the payload, header, padding.
@@ -525,18 +571,41 @@ int check_layout(const kvssd_record_layout* l, Layout* out) {
   return 0;
 }
 
+// the register form needs group_size 32, a 16-byte aligned source and 4-byte
+// aligned packed output (every group then starts aligned)
+inline bool register_groups(int group_size, const void* src, const void* packed) {
+  return group_size == kRegGroup && (reinterpret_cast<uintptr_t>(src) & 15u) == 0 &&
+         (reinterpret_cast<uintptr_t>(packed) & 3u) == 0;
+}
+
 template <typename T>
 void launch_quantize_t(const void* x, int64_t groups, int group_size, int bits, uint8_t* packed, uint16_t* scales,
                        hipStream_t s) {
-  const int64_t blocks = (groups + 255) / 256;
-  hipLaunchKernelGGL(quantize_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, static_cast<const T*>(x),
-                     groups, group_size, bits, packed, scales);
+  const dim3 grid(static_cast<unsigned>((groups + 255) / 256));
+  const T* src = static_cast<const T*>(x);
+  if (register_groups(group_size, x, packed) && bits == 4) {
+    hipLaunchKernelGGL((quantize_kernel<T, 4>), grid, dim3(256), 0, s, src, groups, group_size, bits, packed, scales);
+  } else if (register_groups(group_size, x, packed) && bits == 2) {
+    hipLaunchKernelGGL((quantize_kernel<T, 2>), grid, dim3(256), 0, s, src, groups, group_size, bits, packed, scales);
+  } else {
+    hipLaunchKernelGGL((quantize_kernel<T, 0>), grid, dim3(256), 0, s, src, groups, group_size, bits, packed, scales);
+  }
 }
 
 template <typename T>
 void launch_encode_t(const EncodeParams& p, hipStream_t s) {
   const int64_t groups = 2LL * p.lay.block_tokens * p.lay.kv_heads * (p.lay.head_dim / p.lay.group_size) * p.n;
-  hipLaunchKernelGGL(encode_payload_kernel<T>, dim3(static_cast<unsigned>((groups + 255) / 256)), dim3(256), 0, s, p);
+  const dim3 grid(static_cast<unsigned>((groups + 255) / 256));
+  // records are 4-byte aligned (checked), so every packed group is too
+  const bool reg = register_groups(p.lay.group_size, p.keys, p.records) &&
+                   (reinterpret_cast<uintptr_t>(p.values) & 15u) == 0;
+  if (reg && p.lay.bits == 4) {
+    hipLaunchKernelGGL((encode_payload_kernel<T, 4>), grid, dim3(256), 0, s, p);
+  } else if (reg && p.lay.bits == 2) {
+    hipLaunchKernelGGL((encode_payload_kernel<T, 2>), grid, dim3(256), 0, s, p);
+  } else {
+    hipLaunchKernelGGL((encode_payload_kernel<T, 0>), grid, dim3(256), 0, s, p);
+  }
 }
 
 }  // namespace

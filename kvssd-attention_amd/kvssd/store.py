@@ -3,7 +3,10 @@
 ``create`` quantises each layer's padded ``[T, KVH, D]`` tensor in one call and
 slices it into records.  Groups run along the last dimension only, so this is
 byte-identical to the reference's per-block quantisation (store.py:46-60) while
-avoiding one small quantiser call per block.
+avoiding one small quantiser call per block.  Keys and values that live on a
+GPU are quantised, packed and checksummed there (``records_hip.encode_records``,
+one launch pair per layer, byte-identical records); only the finished records
+cross PCIe.
 """
 
 from __future__ import annotations
@@ -61,6 +64,8 @@ class KVCacheStore:
         n_blocks = -(-tokens // bt)
         block_shape = (bt, spec.kv_heads, spec.head_dim)
         entries: list[BlockEntry] = []
+        if keys.device.type == "cuda" or values.device.type == "cuda":
+            return cls._create_on_gpu(root, keys, values, spec, storage_backend)
         with (root / DATA_FILE).open("wb") as out:
             for layer in range(spec.layers):
                 padded = []
@@ -87,6 +92,36 @@ class KVCacheStore:
                     offset = out.tell()
                     out.write(record)
                     entries.append(BlockEntry(layer, block_id, offset, len(record), valid, crc))
+        manifest = Manifest(spec=spec, entries=entries)
+        manifest.save(root / MANIFEST_FILE)
+        return cls(root, manifest, storage_backend)
+
+    @classmethod
+    def _create_on_gpu(
+        cls,
+        root: Path,
+        keys: torch.Tensor,
+        values: torch.Tensor,
+        spec: CacheSpec,
+        storage_backend: str | StorageBackend | None,
+    ) -> "KVCacheStore":
+        from .records_hip import encode_records
+
+        device = keys.device if keys.device.type == "cuda" else values.device
+        keys, values = keys.to(device), values.to(device)
+        tokens = keys.shape[1]
+        rb = spec.record_bytes
+        entries: list[BlockEntry] = []
+        with (root / DATA_FILE).open("wb") as out:
+            for layer in range(spec.layers):
+                records, crcs = encode_records(keys[layer], values[layer], spec, layer)
+                host = records.cpu()
+                crc_list = crcs.cpu().tolist()
+                for block_id in range(host.shape[0]):
+                    offset = out.tell()
+                    out.write(memoryview(host[block_id].numpy()))
+                    valid = min(spec.block_tokens, tokens - block_id * spec.block_tokens)
+                    entries.append(BlockEntry(layer, block_id, offset, rb, valid, int(crc_list[block_id])))
         manifest = Manifest(spec=spec, entries=entries)
         manifest.save(root / MANIFEST_FILE)
         return cls(root, manifest, storage_backend)

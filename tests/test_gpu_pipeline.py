@@ -214,3 +214,24 @@ def test_host_staged_1m_tokens(cuda_device):
     ref_out, ref_lse = O.attention(query.float().cpu().numpy(), pk, pv, sk, sv, valid, 4, 32, scale, threads=16)
     np.testing.assert_allclose(out.cpu().numpy(), ref_out, atol=ATOL, rtol=RTOL)
     np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_store_created_on_gpu_is_byte_identical(cuda_device, tmp_path: Path, bits: int):
+    # device keys / values are encoded on the GPU; the data file and the
+    # manifest equal those of the CPU quantiser, and the pipeline reads them
+    gen = torch.Generator().manual_seed(31 + bits)
+    keys = torch.randn(2, 1000, 8, 128, generator=gen, dtype=torch.float16)
+    values = torch.randn(2, 1000, 8, 128, generator=gen, dtype=torch.float16)
+    spec = CacheSpec(2, 8, 128, 128, bits, 32)
+    cpu = KVCacheStore.create(tmp_path / "cpu", keys, values, spec)
+    gpu = KVCacheStore.create(tmp_path / "gpu", keys.to(cuda_device), values.to(cuda_device), spec)
+    assert (tmp_path / "cpu" / "blocks.kvssd").read_bytes() == (tmp_path / "gpu" / "blocks.kvssd").read_bytes()
+    assert cpu.manifest.entries == gpu.manifest.entries
+    query = torch.randn(32, 128, generator=gen, dtype=torch.float16)
+    with KVSSDPipeline(gpu, device=cuda_device, stage_blocks=3, attention_backend="hip") as pipe:
+        out = pipe.decode(query, 1)
+    pk, sk, valid = O.quantize_blocks(keys[1].float().numpy(), bits, 32, 128)
+    pv, sv, _ = O.quantize_blocks(values[1].float().numpy(), bits, 32, 128)
+    ref, _ = O.attention(query.float().numpy(), pk, pv, sk, sv, valid, bits, 32, 1 / math.sqrt(128))
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)

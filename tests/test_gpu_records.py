@@ -210,3 +210,19 @@ def test_gather_records_unaligned_outputs(cuda_device):
     got = R.gather_records(raw, spec, n, out=(pk, pv, sk, sv, valid, status))
     for a, b in zip(got, want):
         assert torch.equal(a.view(torch.uint8) if a.dtype == torch.float16 else a, b.view(torch.uint8) if b.dtype == torch.float16 else b)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_quantize_unaligned_source_matches(cuda_device, bits):
+    # a source that is not 16-byte aligned takes the element-wise form; the
+    # register form (aligned, group 32) gives the same bytes
+    gen = torch.Generator().manual_seed(21)
+    x = torch.randn(301, 128, generator=gen).half()
+    buf = torch.empty(301 * 128 + 1, dtype=torch.float16, device=cuda_device)
+    shifted = buf[1:].view(301, 128)
+    shifted.copy_(x.to(cuda_device))
+    a = R.quantize(shifted, bits, 32)
+    b = R.quantize(x.to(cuda_device), bits, 32)
+    packed, scales = oracle_quantize(x, bits, 32)
+    assert torch.equal(a.packed, b.packed) and np.array_equal(a.packed.cpu().numpy(), packed)
+    assert np.array_equal(a.scales.cpu().numpy().view(np.uint16), scales.view(np.uint16))
