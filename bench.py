@@ -61,6 +61,10 @@ HOST_STAGED = {
 CODEC = {
     "gather_int4_128k": ("gather", 131072, 4),
     "encode_int4_128k": ("encode", 131072, 4),
+    # vLLM block records: 8,388,608 fp16 values (a 64-token block of 32 layers,
+    # 8 kv heads, head_dim 128, K and V) as one KVVLLM02 record
+    "vllm_encode_int4_8m": ("vllm_encode", 8388608, 4),
+    "vllm_decode_int4_8m": ("vllm_decode", 8388608, 4),
 }
 KV_HEADS, HEAD_DIM, BLOCK_TOKENS, GROUP = 8, 128, 128, 32
 
@@ -158,6 +162,8 @@ def codec(torch, dev, args) -> int:
     from kvssd.records_hip import encode_records, gather_records
 
     kind, tokens, bits = CODEC[args.workload]
+    if kind.startswith("vllm"):
+        return vllm_codec(torch, dev, args, kind, tokens, bits)
     spec = CacheSpec(1, KV_HEADS, HEAD_DIM, BLOCK_TOKENS, bits, GROUP)
     nb = tokens // BLOCK_TOKENS
     gen = torch.Generator(device=dev).manual_seed(7)
@@ -226,6 +232,65 @@ def codec(torch, dev, args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": name},
         "ok": ok,
+    }), flush=True)
+    return 0
+
+
+def vllm_codec(torch, dev, args, kind, elements, bits) -> int:
+    """Encode (fp16 values -> record) or decode (record -> fp16 values, CRC
+    checked) of one vLLM block on the GPU; copies rotate past the Infinity Cache."""
+    from kvssd import vllm_codec_hip as V
+
+    gen = torch.Generator(device=dev).manual_seed(7)
+    copies = args.copies or 8
+    vals = [torch.randn(elements, generator=gen, device=dev, dtype=torch.float16) for _ in range(copies)]
+    recs = [V.encode_vllm_block(v, bits=bits, group_size=GROUP) for v in vals]
+    payload = elements // GROUP * 2 + elements * bits // 8
+    outs = [torch.empty_like(v) for v in vals]
+    if kind == "vllm_encode":
+        def launch(i):
+            V.encode_vllm_block(vals[i % copies], bits=bits, group_size=GROUP)
+
+        nbytes = elements * 2 + recs[0].numel()  # values read, record written
+        name = "quantize_kernel + vllm_rows_kernel + vllm_combine_kernel"
+    else:
+        def launch(i):
+            V.decode_vllm_block(recs[i % copies], outs[i % copies])
+
+        nbytes = payload + elements * 2  # payload read, values written
+        name = "vllm_rows_kernel + vllm_combine_kernel"
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for i in range(args.steps):
+        evs[i][0].record(stream)
+        launch(i)  # decode reads its CRC status back, so each step synchronises
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    med = sorted(a.elapsed_time(b) for a, b in evs)[args.steps // 2]
+    V.decode_vllm_block(recs[0], outs[0])
+    err = float((outs[0].float() - vals[0].float()).abs().max())
+    gbps = nbytes / (med * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": f"vLLM block {kind.split('_')[1]} GB/s (algorithmic bytes), INT4, {elements} fp16 values",
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(med, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "elements": elements, "bits": bits, "group_size": GROUP,
+                   "record_bytes": recs[0].numel(), "alg_bytes_per_step": nbytes, "copies_rotated": copies},
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None, "kernel": name},
+        "max_abs_round_trip": err,
     }), flush=True)
     return 0
 

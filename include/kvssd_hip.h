@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KVSSD_HIP_ABI_VERSION 2
+#define KVSSD_HIP_ABI_VERSION 3
 
 /* Query element types accepted by kvssd_hip_fused_decode (the reference
  * dispatches fp32/fp64/fp16/bf16 queries: csrc/fused_decode.cu:131-133). */
@@ -179,6 +179,29 @@ int kvssd_hip_quantize(const void* x, int dtype, int64_t rows, int head_dim, int
 int kvssd_hip_encode_records(const kvssd_record_layout* layout, int dtype, const void* keys, const void* values,
                              int64_t tokens, int layer, int first_block, uint8_t* records, uint32_t* crcs,
                              void* stream);
+
+/* vLLM block records (src/kvssd/integrations/vllm_codec.py:18-102): a 32-byte
+ * header "<8sBBBBIIQI" ("KVVLLM02", version 1, bits, dtype code 1/2/3 for
+ * float16/bfloat16/float32, 0, group_size, elements, payload bytes, CRC-32),
+ * payload = fp16 scales [elements / group_size] | codes [elements * bits / 8]
+ * of the block's values as one flat vector, zero padding to a 4096 multiple.
+ * Record size and the device scratch bytes kvssd_hip_vllm_encode / _decode
+ * need for a block of `elements` values (payload at most 16 MiB). */
+int kvssd_hip_vllm_sizes(int64_t elements, int bits, int group_size, size_t* record_bytes, size_t* scratch_bytes);
+
+/* encode_vllm_block (vllm_codec.py:42-70) on the GPU: `elements` values of
+ * `dtype` (F16, BF16 or F32) -> the whole record at `record` (4-byte aligned,
+ * kvssd_hip_vllm_sizes bytes) and its payload CRC-32 in *crc (device). */
+int kvssd_hip_vllm_encode(const void* values, int dtype, int64_t elements, int bits, int group_size, uint8_t* record,
+                          uint32_t* crc, void* scratch, size_t scratch_bytes, void* stream);
+
+/* The GPU half of decode_vllm_block (vllm_codec.py:73-102): the caller has
+ * parsed and checked the header (magic, version, dtype, payload length); this
+ * verifies the payload CRC-32 against `crc` (*status = 0, or 3 on a mismatch)
+ * and dequantises the codes into `destination` (`elements` values of `dtype`),
+ * (code - mid) * scale in fp32 rounded once, as dequantize_tensor(q, dtype). */
+int kvssd_hip_vllm_decode(const uint8_t* payload, int64_t elements, int bits, int group_size, uint32_t crc, int dtype,
+                          void* destination, int32_t* status, void* scratch, size_t scratch_bytes, void* stream);
 
 /* hipMemcpyAsync host->device of `bytes` bytes on `stream`; `src` should be
  * page-locked for the copy to be asynchronous.  The staging copy of

@@ -287,6 +287,27 @@ __attribute__((visibility("default"))) int kvssd_hip_encode_records(const kvssd_
                                static_cast<hipStream_t>(stream));
 }
 
+__attribute__((visibility("default"))) int kvssd_hip_vllm_sizes(int64_t elements, int bits, int group_size,
+                                                                size_t* record_bytes, size_t* scratch_bytes) {
+  return vllm_sizes(elements, bits, group_size, record_bytes, scratch_bytes);
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_vllm_encode(const void* values, int dtype, int64_t elements,
+                                                                 int bits, int group_size, uint8_t* record,
+                                                                 uint32_t* crc, void* scratch, size_t scratch_bytes,
+                                                                 void* stream) {
+  return launch_vllm_encode(values, dtype, elements, bits, group_size, record, crc, scratch, scratch_bytes,
+                            static_cast<hipStream_t>(stream));
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_vllm_decode(const uint8_t* payload, int64_t elements, int bits,
+                                                                 int group_size, uint32_t crc, int dtype,
+                                                                 void* destination, int32_t* status, void* scratch,
+                                                                 size_t scratch_bytes, void* stream) {
+  return launch_vllm_decode(payload, elements, bits, group_size, crc, dtype, destination, status, scratch,
+                            scratch_bytes, static_cast<hipStream_t>(stream));
+}
+
 __attribute__((visibility("default"))) int kvssd_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes,
                                                                       void* stream) {
   if (bytes == 0) return 0;

@@ -63,6 +63,13 @@ int launch_quantize(const void* x, int dtype, int64_t rows, int head_dim, int bi
 int launch_encode_records(const kvssd_record_layout* layout, int dtype, const void* keys, const void* values,
                           int64_t tokens, int layer, int first_block, uint8_t* records, uint32_t* crcs,
                           hipStream_t stream);
+// ---- vLLM block codec (vllm_codec.hip)
+int vllm_sizes(int64_t elements, int bits, int group_size, size_t* record_bytes, size_t* scratch_bytes);
+int launch_vllm_encode(const void* values, int dtype, int64_t elements, int bits, int group_size, uint8_t* record,
+                       uint32_t* crc, void* scratch, size_t scratch_bytes, hipStream_t stream);
+int launch_vllm_decode(const uint8_t* payload, int64_t elements, int bits, int group_size, uint32_t expected_crc,
+                       int dtype, void* destination, int32_t* status, void* scratch, size_t scratch_bytes,
+                       hipStream_t stream);
 int launch_unpack_codes(const uint8_t* packed, int bits, int64_t n_bytes, uint8_t* codes, hipStream_t stream);
 int launch_dequantize(const uint8_t* packed, const uint16_t* scales, int64_t rows, int head_dim, int bits,
                       int group_size, float* out, hipStream_t stream);

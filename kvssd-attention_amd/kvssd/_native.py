@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
 LIB_PATH = Path(__file__).resolve().parent / "libkvssd_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_GENERAL, KERNEL_MFMA, KERNEL_STAGED, KERNEL_PAIRS = 0, 1, 2, 3, 4
@@ -75,6 +75,9 @@ SIGNATURES = {
     "kvssd_hip_gather_records": (_I, [ctypes.POINTER(RecordLayout), _VP, _SZ, _I, _I] + [_VP] * 7),
     "kvssd_hip_quantize": (_I, [_VP, _I, _I64, _I, _I, _I, _VP, _VP, _VP]),
     "kvssd_hip_encode_records": (_I, [ctypes.POINTER(RecordLayout), _I, _VP, _VP, _I64, _I, _I, _VP, _VP, _VP]),
+    "kvssd_hip_vllm_sizes": (_I, [_I64, _I, _I, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "kvssd_hip_vllm_encode": (_I, [_VP, _I, _I64, _I, _I, _VP, _VP, _VP, _SZ, _VP]),
+    "kvssd_hip_vllm_decode": (_I, [_VP, _I64, _I, _I, ctypes.c_uint32, _I, _VP, _VP, _VP, _SZ, _VP]),
     "kvssd_hip_memcpy_h2d_async": (_I, [_VP, _VP, _SZ, _VP]),
     "kvssd_hip_last_error": (ctypes.c_char_p, []),
 }

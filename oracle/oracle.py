@@ -216,6 +216,37 @@ def crc32_zlib(data: bytes) -> int:
     return zlib.crc32(data)
 
 
+# ------------------------------------------------------------ vLLM block ---
+
+# Restated from src/kvssd/integrations/vllm_codec.py:18-21.
+VLLM_MAGIC = b"KVVLLM02"
+VLLM_HEADER = struct.Struct("<8sBBBBIIQI")
+
+
+def encode_vllm_record(values: np.ndarray, bits: int, group_size: int, dtype_code: int) -> bytes:
+    """encode_vllm_block (src/kvssd/integrations/vllm_codec.py:42-70): the block's
+    values as one flat vector quantised groupwise; payload = fp16 scales | packed
+    codes; 32-byte header; zero padding to a 4096 multiple.  ``values`` are the
+    block's values converted to float32 (quantize_tensor works on x.float())."""
+    flat = np.ascontiguousarray(values, dtype=np.float32).reshape(-1)
+    codes, scales = quantize_np(flat, bits, group_size)
+    payload = scales.astype(np.float16).tobytes() + pack_np(codes, bits).tobytes()
+    head = VLLM_HEADER.pack(VLLM_MAGIC, 1, bits, dtype_code, 0, group_size, flat.size, len(payload), crc32(payload))
+    rec = head + payload
+    return rec + bytes(-(-len(rec) // ALIGNMENT) * ALIGNMENT - len(rec))
+
+
+def decode_vllm_values(record: bytes) -> np.ndarray:
+    """The float32 values decode_vllm_block dequantises (vllm_codec.py:73-102,
+    before the cast to the record's dtype): (code - mid) * scale per group."""
+    _, _, bits, _, _, g, elements, plen, _ = VLLM_HEADER.unpack_from(record)
+    payload = record[VLLM_HEADER.size : VLLM_HEADER.size + plen]
+    nscale = elements // g
+    scales = np.frombuffer(payload[: 2 * nscale], dtype=np.float16)
+    codes = unpack_np(np.frombuffer(payload[2 * nscale :], dtype=np.uint8), bits, elements)
+    return dequantize_np(codes, scales, bits, g)
+
+
 # -------------------------------------------------------------- attention ---
 
 

@@ -20,6 +20,10 @@ attention                    torch float64 scaled_dot_product_attention on the
 merge                        split-anywhere invariant against one full call
 selectors                    closed-form known answers
 record format                struct layout, CacheSpec sizes (151552 / 86016)
+vLLM block record            hand-assembled known answer (header fields, scale
+                             and code bytes, zlib CRC, padding); decode of the
+                             known answer gives the closed-form values; decode
+                             inverts encode to within half a quantisation step
 """
 
 from __future__ import annotations
@@ -315,3 +319,31 @@ def test_record_layout_known_answers():
     assert fields[11] == zlib.crc32(payload)
     assert payload[:8] == ks.tobytes() and payload[16:32] == kp.tobytes()
     assert rec[52 + fields[10] :] == bytes(4096 - 52 - fields[10])
+
+
+# ------------------------------------------------------------- vLLM block ---
+
+
+def test_vllm_record_known_answer():
+    # [7, -7, 0, 0] with g=4, INT4: scale 7/7 = 1.0 (fp16 0x3C00), codes
+    # [15, 1, 8, 8] -> packed low nibble first [0x1F, 0x88]
+    rec = O.encode_vllm_record(np.array([7.0, -7.0, 0.0, 0.0]), 4, 4, 1)
+    payload = bytes([0x00, 0x3C, 0x1F, 0x88])
+    head = struct.pack("<8sBBBBIIQI", b"KVVLLM02", 1, 4, 1, 0, 4, 4, 4, zlib.crc32(payload))
+    assert len(rec) == 4096
+    assert rec[:32] == head and rec[32:36] == payload and rec[36:] == bytes(4096 - 36)
+    assert O.decode_vllm_values(rec).tolist() == [7.0, -7.0, 0.0, 0.0]
+    # INT2, g=4: [1, -1, 0.4, -0.6] -> scale 1.0, codes [3, 1, 2, 1] -> 0b01_10_01_11
+    rec2 = O.encode_vllm_record(np.array([1.0, -1.0, 0.4, -0.6]), 2, 4, 3)
+    assert rec2[32:35] == bytes([0x00, 0x3C, 0x67])
+    assert struct.unpack_from("<8sBBBBIIQI", rec2)[7] == 3
+    assert O.decode_vllm_values(rec2).tolist() == [1.0, -1.0, 0.0, -1.0]
+
+
+def test_vllm_record_round_trip_bound():
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(4096).astype(np.float32)
+    rec = O.encode_vllm_record(x, 4, 32, 3)
+    y = O.decode_vllm_values(rec)
+    step = np.abs(x.reshape(-1, 32)).max(axis=1, keepdims=True) / 7
+    assert np.all(np.abs((y - x).reshape(-1, 32)) <= step * 0.5 + 1e-3 * step)
