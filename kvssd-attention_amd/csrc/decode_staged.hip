@@ -393,48 +393,125 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   const int kvh0 = grp * kKG;
   const int head0 = (kvh0 + w) * p.gq;
 
-  // The first stage's copies go out before anything else: the split's first
-  // attended block, tokens 0..127 (one scalar read with a block table).  If
-  // that block holds no valid token they are simply not used.
   const CopyMap<BITS> cm = make_copy_map<BITS>(wave, lane, p.kv_heads);
   const uint32_t lds0 = lds_addr(lds);
-  bool spec = false;
-  if (u_begin < u_end) {
-    Cursor c0{0, __builtin_amdgcn_readfirstlane(p.table ? p.table[u_begin] : u_begin), 0, 0};
-    if (c0.blk >= 0 && c0.blk < p.num_blocks) {
-      issue_stage<BITS>(p, lds0, c0, kvh0, wave, cm);
-      spec = true;
-    }
-  }
-
-  // the query loads go out next: they complete in issue order, right after
-  // the first stage's copies, instead of a round trip after them
-  const QueryRaw<QUADS> qraw = coop_query_load<BITS, QUADS, QT>(p.query, p.gq, head0, lane);
-
-  // the split's (block id, clamped valid count) list, read once into LDS
   int* units = reinterpret_cast<int*>(lds + 2 * G::STAGE + kWBytes);
   const int n_units = max(0, u_end - u_begin);  // <= kMaxUnits, checked on the host
-  for (int i = threadIdx.x; i < n_units; i += kThreads) {
-    const int blk = p.table ? p.table[u_begin + i] : u_begin + i;
-    units[2 * i] = blk;
-    units[2 * i + 1] = (blk < 0 || blk >= p.num_blocks) ? 0 : clamp_valid(p.valid[blk], p.block_tokens);
-  }
-  __syncthreads();
 
-  Cursor cur{-1, 0, 0, -kStageTok};
-  bool have = next_stage<kStageTok>(cur, units, n_units);
-  if (have && !(spec && cur.u == 0 && cur.sb0 == 0)) {
-    // the first valid stage is elsewhere: let this wave's early copies land
-    // (they target the same LDS chunks), then load the right ones
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    issue_stage<BITS>(p, lds0, cur, kvh0, wave, cm);
-  }
+  // Early form (no block table, the query 16-byte aligned, and room in the
+  // second stage buffer for the query scratch and the workgroup's query
+  // rows): every early memory operation is an LDS copy, so no compiler-placed
+  // wait for a load can also wait for a stage.  The query rows go first, then
+  // stage 0 and the split's valid counts; once the rows land the query
+  // operands are built and stage 1 goes out (~2 us after entry instead of
+  // after stage 0 has landed, ~6 us): the start is latency-bound, and two
+  // stages in flight arrive nearly as soon as one.
+  constexpr int kStageCopies = 2 * G::KV_PER_WAVE + 1;    // copy instructions per wave per stage
+  constexpr int kUnitCopies = kMaxUnits / (64 * kWaves);  // dword copies per wave for the valid counts
+  constexpr int kQBytesMax = kKG * 4 * QUADS * 128 * static_cast<int>(sizeof(QT));
+  constexpr bool kEarlyFits = kWaves * coop_scratch_bytes<QUADS> + kQBytesMax <= G::STAGE;
+  const bool direct = kEarlyFits && p.table == nullptr && (reinterpret_cast<uintptr_t>(p.query) & 15u) == 0;
+  auto advance = [&](Cursor& c) -> bool {
+    return direct ? next_stage_direct<kStageTok>(c, units, u_begin, p.block_tokens, n_units)
+                  : next_stage<kStageTok>(c, units, n_units);
+  };
 
-  // query operands, through per-wave scratch in the second stage buffer (its
-  // first copies go out after the loop's first barrier)
   QueryOps<QUADS, QSPLIT> qo;
+  Cursor cur{-1, 0, 0, -kStageTok};
+  Cursor nxt{-1, 0, 0, -kStageTok};
+  bool have = false, have_n = false;
+  bool pre1 = false;   // stage 1 went out early and is the loop's second stage
+  bool wait0 = true;   // the loop's first pass waits for its stage and meets the barrier
+  bool spec = false;   // stage 0 (the split's first block, tokens 0..127) went out early
+  if (direct) {
+    uint8_t* qrows = lds + 2 * G::STAGE - kQBytesMax;  // tail of the second stage buffer
+    const int qcopies = kKG * p.gq * 128 * static_cast<int>(sizeof(QT)) / 1024;
+    const uint8_t* qsrc =
+        static_cast<const uint8_t*>(p.query) + static_cast<long>(kvh0) * p.gq * 128 * static_cast<long>(sizeof(QT));
+    for (int i = wave; i < qcopies; i += kWaves)
+      dma16<false>(qsrc, 1024u * static_cast<uint32_t>(i) + 16u * static_cast<uint32_t>(lane),
+                   lds_addr(qrows) + 1024u * static_cast<uint32_t>(i));
+    if (n_units > 0) {
+      issue_stage<BITS>(p, lds0, Cursor{0, u_begin, 0, 0}, kvh0, wave, cm);
+      spec = true;
+    }
+    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(p.valid + (n_units > 0 ? u_begin : 0));
+    const int ulast = max(n_units - 1, 0);
+#pragma unroll
+    for (int j = 0; j < kUnitCopies; ++j) {
+      const int i0 = (j * kWaves + wave) * 64;
+      dma4(vsrc, 4u * static_cast<uint32_t>(min(i0 + lane, ulast)), lds_addr(reinterpret_cast<const uint8_t*>(units)) + 4u * static_cast<uint32_t>(i0));
+    }
+    // the query rows (issued first) have landed once at most the later copies are outstanding
+    if (spec) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies + kUnitCopies));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_wait(kUnitCopies));
+    __syncthreads();
+    coop_query_build<BITS, QUADS, QSPLIT>(qo, coop_query_load<BITS, QUADS, QT>(qrows, p.gq, w * p.gq, lane),
+                                          p.scale_log2, lane, lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
+    __syncthreads();  // query rows and scratch consumed: the second buffer is free
+    Cursor c1{-1, 0, 0, 0};
+    bool issued1 = false;
+    if (spec) {
+      if (p.block_tokens > kStageTok) {
+        c1 = Cursor{0, u_begin, 0, kStageTok};
+        issued1 = true;
+      } else if (n_units > 1) {
+        c1 = Cursor{1, u_begin + 1, 0, 0};
+        issued1 = true;
+      }
+      if (issued1) issue_stage<BITS>(p, lds0 + static_cast<uint32_t>(G::STAGE), c1, kvh0, wave, cm);
+    }
+    // stage 0 and the valid counts landed (stage 1 may still be in flight)
+    if (issued1) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies));
+    else __builtin_amdgcn_s_waitcnt(0x0F70);
+    __syncthreads();
+    have = advance(cur);
+    wait0 = false;
+    if (have && !(spec && cur.u == 0 && cur.sb0 == 0)) {
+      // the first valid stage is elsewhere (empty or partial blocks): let this
+      // wave's early copies land, then load the right ones
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      issue_stage<BITS>(p, lds0, cur, kvh0, wave, cm);
+      wait0 = true;
+    }
+    nxt = cur;
+    have_n = have && advance(nxt);
+    pre1 = issued1 && have_n && nxt.blk == c1.blk && nxt.sb0 == c1.sb0;
+    if (issued1 && !pre1) wait0 = true;  // the early stage 1 must land before its buffer is reloaded
+  } else {
+    // The first stage's copies go out before anything else: the split's first
+    // attended block, tokens 0..127 (one scalar read with a block table).  If
+    // that block holds no valid token they are simply not used.
+    if (u_begin < u_end) {
+      Cursor c0{0, __builtin_amdgcn_readfirstlane(p.table ? p.table[u_begin] : u_begin), 0, 0};
+      if (c0.blk >= 0 && c0.blk < p.num_blocks) {
+        issue_stage<BITS>(p, lds0, c0, kvh0, wave, cm);
+        spec = true;
+      }
+    }
+    // the query loads go out next: they complete in issue order, right after
+    // the first stage's copies, instead of a round trip after them
+    const QueryRaw<QUADS> qraw = coop_query_load<BITS, QUADS, QT>(p.query, p.gq, head0, lane);
+    // the split's (block id, clamped valid count) list, read once into LDS
+    for (int i = threadIdx.x; i < n_units; i += kThreads) {
+      const int blk = p.table ? p.table[u_begin + i] : u_begin + i;
+      units[2 * i] = blk;
+      units[2 * i + 1] = (blk < 0 || blk >= p.num_blocks) ? 0 : clamp_valid(p.valid[blk], p.block_tokens);
+    }
+    __syncthreads();
+    have = advance(cur);
+    if (have && !(spec && cur.u == 0 && cur.sb0 == 0)) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);
+      issue_stage<BITS>(p, lds0, cur, kvh0, wave, cm);
+    }
+    // query operands, through per-wave scratch in the second stage buffer (its
+    // first copies go out after the loop's first barrier)
+    coop_query_build<BITS, QUADS, QSPLIT>(qo, qraw, p.scale_log2, lane,
+                                          lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
+    nxt = cur;
+    have_n = have && advance(nxt);
+  }
   static_assert(kWaves * coop_scratch_bytes<QUADS> <= G::STAGE, "query scratch fits a stage buffer");
-  coop_query_build<BITS, QUADS, QSPLIT>(qo, qraw, p.scale_log2, lane, lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
   // masks in VGPRs: p.units >= 1, so (lane & (p.units >> 30)) is 0 but opaque
   const Masks mk = make_masks(static_cast<uint32_t>(lane) & static_cast<uint32_t>(p.units >> 30));
   u32x4 offa[BITS == 4 ? 1 : 2];
@@ -459,13 +536,16 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // ------------------------------------------- double-buffered stage loop
   // the stage after the current one is looked up a step ahead, so that its
   // copies go out right after the barrier
-  Cursor nxt = cur;
-  bool have_n = have && next_stage<kStageTok>(nxt, units, n_units);
   int buf = 0;
+  bool first = true;
   while (have) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
-    __syncthreads();                     // ... everyone's; and the other buffer is free
-    if (have_n) issue_stage<BITS>(p, lds0 + static_cast<uint32_t>((buf ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
+    if (!first || wait0) {
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
+      __syncthreads();                     // ... everyone's; and the other buffer is free
+    }
+    if (have_n && !(first && pre1))
+      issue_stage<BITS>(p, lds0 + static_cast<uint32_t>((buf ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
+    first = false;
     const int hv = min(kStageTok, cur.vb - cur.sb0) - kHalfTok * half;
     if (hv > 0) {
       uint8_t* sbuf = lds + buf * G::STAGE;
@@ -474,7 +554,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     }
     cur = nxt;
     have = have_n;
-    if (have) have_n = next_stage<kStageTok>(nxt, units, n_units);
+    if (have) have_n = advance(nxt);
     buf ^= 1;
   }
 

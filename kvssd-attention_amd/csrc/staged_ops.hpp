@@ -232,6 +232,26 @@ __device__ __forceinline__ bool next_stage(Cursor& c, const int* units, int n_un
   return true;
 }
 
+// As next_stage for a split without a block table: unit u is block
+// u_begin + u and vraw[u] its raw valid count (LDS, copied straight from the
+// valid array), clamped here.
+template <int STAGE_TOK>
+__device__ __forceinline__ bool next_stage_direct(Cursor& c, const int* vraw, int u_begin, int block_tokens,
+                                                  int n_units) {
+  c.sb0 += STAGE_TOK;
+  while (c.sb0 >= c.vb) {
+    if (++c.u >= n_units) return false;
+    c.blk = u_begin + c.u;
+    c.vb = __builtin_amdgcn_readfirstlane(clamp_valid(vraw[c.u], block_tokens));
+    c.sb0 = 0;
+  }
+  return true;
+}
+
+// s_waitcnt immediate waiting until at most n vector-memory operations of
+// this wave are outstanding (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+constexpr int vmcnt_wait(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
 // ----------------------------------------------------------- query set-up ---
 template <int QUADS, int QSPLIT>
 struct QueryOps {

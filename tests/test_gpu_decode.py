@@ -297,3 +297,26 @@ def test_int2_8_byte_aligned_buffers_use_mfma_kernel(cuda_device):
     out, lse = auto.run(query, moved, 0.1)
     assert auto.last_kernel == "mfma"
     check(out, lse, ref_out, ref_lse)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_many_blocks_with_empty_and_partial_split_starts(cuda_device, bits):
+    # 2048 blocks of 128 tokens: every split holds many blocks; zero and
+    # partial valid counts at and right after split starts exercise the
+    # staged kernel's early-copy speculation (first and second stage re-issued)
+    rng = np.random.default_rng(41 + bits)
+    nb = 2048
+    q, pk, pv, sk, sv, _ = make_batch(5, 16, 4, 128, nb, 128, bits, 32)
+    valid = rng.integers(1, 129, nb).astype(np.int32)
+    valid[::4] = 0
+    valid[1::8] = rng.integers(0, 3, nb // 8)
+    valid[-5:] = 0
+    for qdtype in (torch.float32, torch.float16):
+        qq = torch.from_numpy(q).to(qdtype).float().numpy()
+        ref_out, ref_lse = O.attention(qq, pk, pv, sk, sv, valid, bits, 32, 0.1, threads=16)
+        query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, qdtype=qdtype)
+        names = kernels_for(query, batch)
+        assert "staged" in names
+        for kernel in names:
+            out, lse = HipAttentionBackend(kernel).run(query, batch, 0.1)
+            check(out, lse, ref_out, ref_lse)
