@@ -58,3 +58,28 @@ def test_kernel_choice_is_reported():
     assert k.value == _native.KERNEL_GENERAL
     desc.kernel = _native.KERNEL_GENERAL
     assert lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(k)) == 0
+
+
+def test_record_codec_sizes_and_argument_errors():
+    # sizes and argument checks of the record and vLLM codecs need no GPU
+    lib = _native.load()
+    n = ctypes.c_size_t(0)
+    lay = _native.RecordLayout(4, 128, 8, 128, 32)
+    assert lib.kvssd_hip_record_bytes(ctypes.byref(lay), ctypes.byref(n)) == 0 and n.value == 151552
+    lay2 = _native.RecordLayout(2, 128, 8, 128, 32)
+    assert lib.kvssd_hip_record_bytes(ctypes.byref(lay2), ctypes.byref(n)) == 0 and n.value == 86016
+    bad = _native.RecordLayout(3, 128, 8, 128, 32)
+    assert lib.kvssd_hip_record_bytes(ctypes.byref(bad), ctypes.byref(n)) < 0
+    assert "bits" in _native.last_error()
+    st = (ctypes.c_int32 * 1)()
+    assert lib.kvssd_hip_gather_records(ctypes.byref(lay), None, 151552, 1, 1, *([None] * 6), st, None) < 0
+    assert lib.kvssd_hip_gather_records(ctypes.byref(lay), 4, 100, 1, 1, *([8] * 6), st, None) < 0  # stride too small
+    assert lib.kvssd_hip_quantize(None, 0, 4, 100, 4, 32, None, None, None) < 0  # 100 % 32
+    rec, scratch = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert lib.kvssd_hip_vllm_sizes(8388608, 4, 32, ctypes.byref(rec), ctypes.byref(scratch)) == 0
+    assert rec.value == 4722688 and scratch.value == 288 * 4 + 4  # 4,718,592-byte payload: 288 rows
+    assert lib.kvssd_hip_vllm_sizes(40, 4, 32, ctypes.byref(rec), ctypes.byref(scratch)) < 0
+    assert "not divisible by group_size=32" in _native.last_error()
+    assert lib.kvssd_hip_vllm_sizes(1 << 27, 4, 32, ctypes.byref(rec), ctypes.byref(scratch)) < 0  # > 16 MiB payload
+    assert lib.kvssd_hip_vllm_encode(None, 3, 64, 4, 32, None, None, None, 0, None) < 0  # float64
+    assert lib.kvssd_hip_vllm_decode(None, 64, 4, 32, 0, 0, None, None, None, 0, None) < 0
