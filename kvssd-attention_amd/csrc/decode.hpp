@@ -38,6 +38,9 @@ int launch_mfma(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts)
 
 // ---- LDS-staged matrix-core kernel: the matrix-core shapes with kv_heads % 4 == 0
 bool staged_supported(const kvssd_decode_desc& d, std::string* why);
+// whether the staged kernel takes 8 kv heads per workgroup for this shape
+// (the split plan doubles its work items then)
+bool staged_wide(const kvssd_decode_desc& d, int units);
 bool staged_aligned(const DecodeArgs& a);
 int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts);
 

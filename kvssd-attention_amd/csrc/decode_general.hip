@@ -187,8 +187,10 @@ SplitPlan plan_splits(const kvssd_decode_desc& d, int units) {
   // about 1024 (kv head, split) work items: one resident round of the
   // matrix-core kernel (4 single-wave workgroups per CU on a 256-CU part, each
   // streaming its blocks with loads one sub-block ahead); the general kernel
-  // runs 1024+ four-wave workgroups
-  long per = (static_cast<long>(units) * d.kv_heads + 1023) / 1024;
+  // runs 1024+ four-wave workgroups.  2048 where the staged kernel gives each
+  // workgroup all 8 kv heads of a row: 256 workgroups either way.
+  const long items = staged_wide(d, units) ? 2048 : 1024;
+  long per = (static_cast<long>(units) * d.kv_heads + items - 1) / items;
   SplitPlan plan{};
   plan.blocks_per_split = static_cast<int>(per < 1 ? 1 : per);
   plan.splits = (units + plan.blocks_per_split - 1) / plan.blocks_per_split;

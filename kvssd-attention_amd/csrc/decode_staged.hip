@@ -6,22 +6,27 @@
 // src/kvssd/backends/reference.py:22-50; element addressing of
 // csrc/fused_decode.cu:50-56).
 //
-// Work split.  A workgroup of 8 waves owns 4 consecutive kv heads (a "group")
-// and one split (a range of attended blocks).  It walks the split in stages of
-// 128 tokens; wave (w, half) computes kv head w of the group over tokens
-// 64*half .. 64*half+63 of every stage, and the two halves meet in LDS at the
-// end, so each workgroup writes one partial per query head of its group.
+// Work split.  A workgroup of 8 waves owns KG consecutive kv heads (a
+// "group": 4, or 8 when kv_heads % 8 == 0 and the context is long enough to
+// fill the chip) and one split (a range of attended blocks).  It walks the
+// split in stages of 512 / KG tokens (128 or 64); wave (w, half) computes kv
+// head w of the group over tokens 64*half .. 64*half+63 of every stage.  With
+// KG = 4 the two halves meet in LDS at the end; with KG = 8 there is one half.
+// Each workgroup writes one partial per query head of its group.  Whole
+// 512-byte token rows per workgroup (KG = 8, INT4, 8 kv heads) keep every
+// workgroup's copies spread evenly over the memory channels.
 //
-// Staging.  The packed rows of 4 kv heads of one token are contiguous in HBM
-// ([blocks][tokens][kv_heads][packed]), so a stage is four contiguous streams
-// (K codes, V codes, K scales, V scales).  They are copied HBM -> LDS with
-// global_load_lds_dwordx4 (16 bytes per lane, 1 KB per instruction, no VGPRs
-// held while in flight), double-buffered: stage i+1's copies are issued right
-// after the barrier that opens stage i, so they overlap all of stage i's math.
-// LDS per stage: 72 KB (INT4) / 40 KB (INT2), i.e. 144 KB / 80 KB in total.
+// Staging.  The packed rows of the group's kv heads of one token are
+// contiguous in HBM ([blocks][tokens][kv_heads][packed]), so a stage is four
+// contiguous streams (K codes, V codes, K scales, V scales).  They are copied
+// HBM -> LDS with global_load_lds_dwordx4 (16 bytes per lane, 1 KB per
+// instruction, no VGPRs held while in flight), double-buffered: stage i+1's
+// copies are issued right after the barrier that opens stage i, so they
+// overlap all of stage i's math.  LDS per stage: 72 KB (INT4) / 40 KB (INT2),
+// i.e. 144 KB / 80 KB in total, whatever KG.
 //
 // LDS layout.  A region stores, per token t of the stage, CPT 16-byte chunks
-// (CPT = 4 kv heads x packed bytes / 16); chunk idx of token t sits at
+// (CPT = KG kv heads x packed bytes / 16); chunk idx of token t sits at
 // position t*CPT + (idx ^ phi(t)).  phi is chosen so that the matrix-core
 // operand reads below hit 16 distinct bank groups per 16 lanes; the DMA lane
 // -> global address map applies the inverse, so each copy instruction still
@@ -55,19 +60,21 @@
 namespace kvssd {
 namespace {
 
-constexpr int kKG = 4;               // kv heads per workgroup
-constexpr int kWaves = 2 * kKG;      // (kv head, token half)
+constexpr int kWaves = 8;            // (kv head, token half)
 constexpr int kThreads = 64 * kWaves;
-constexpr int kStageTok = 128;       // tokens per stage
 constexpr int kHalfTok = 64;         // tokens per wave per stage
 constexpr int kMaxUnits = 2048;      // attended blocks per split (block list kept in LDS)
+template <int KG>
+constexpr int kStageTok = kWaves / KG * kHalfTok;  // tokens per stage: 128 (KG 4) or 64 (KG 8)
 
-template <int BITS>
+template <int BITS, int KG>
 struct Geo {
   static constexpr int PD = 128 * BITS / 8;               // packed bytes per kv-head row
-  static constexpr int CPT = kKG * PD / 16;               // chunks per token row of the group
-  static constexpr int KV_BYTES = kStageTok * kKG * PD;   // one code region
-  static constexpr int SC_BYTES = kStageTok * kKG * 8;    // one scale region
+  static constexpr int CPT = KG * PD / 16;                // chunks per token row of the group
+  static constexpr int SCPT = KG * 8 / 16;                // chunks per scale row of the group
+  static constexpr int HALVES = kWaves / KG;
+  static constexpr int KV_BYTES = kStageTok<KG> * KG * PD;  // one code region
+  static constexpr int SC_BYTES = kStageTok<KG> * KG * 8;   // one scale region
   static constexpr int K_OFF = 0;
   static constexpr int V_OFF = KV_BYTES;
   static constexpr int SK_OFF = 2 * KV_BYTES;
@@ -80,7 +87,9 @@ struct Geo {
   // INT2 K chunks are too few for two query quads, so W gets its own region.
   static constexpr bool W_IN_K = BITS == 4;
 };
-static_assert(Geo<4>::SC_INST * 2 == kWaves && Geo<2>::SC_INST * 2 == kWaves, "one scale copy per wave");
+static_assert(Geo<4, 4>::SC_INST * 2 == kWaves && Geo<2, 4>::SC_INST * 2 == kWaves && Geo<4, 8>::SC_INST * 2 == kWaves &&
+                  Geo<2, 8>::SC_INST * 2 == kWaves,
+              "one scale copy per wave");
 
 struct StagedParams {
   const void* query;
@@ -97,11 +106,14 @@ struct StagedParams {
 };
 
 // XOR swizzle of a region's chunk index for token t (CPT chunks per token).
+// A token row of 16 or more chunks spans every bank group, so the swizzle
+// only permutes its low 4 bits (the same for CPT 16 and 32).
 template <int CPT>
 __device__ __forceinline__ int phi(int t) {
-  if constexpr (CPT == 16) return (t & 15) ^ (((t >> 4) & 3) << 2);
+  if constexpr (CPT >= 16) return (t & 15) ^ (((t >> 4) & 3) << 2);
   else if constexpr (CPT == 8) return ((t & 15) >> 1) ^ (((t >> 4) & 3) << 1);
-  else return (t >> 3) & 1;  // CPT == 2: scale rows
+  else if constexpr (CPT == 4) return (t >> 2) & 3;  // scale rows of 8 kv heads
+  else return (t >> 3) & 1;                          // CPT == 2: scale rows of 4 kv heads
 }
 
 template <int CPT>
@@ -111,16 +123,16 @@ __device__ __forceinline__ int chunk_byte(int t, int idx) {
 
 // Per-lane byte offsets (relative to the stage's group base) of this wave's
 // copy instructions: code regions (same map for K and V) and one scale copy.
-template <int BITS>
+template <int BITS, int KG>
 struct CopyMap {
-  uint32_t kv[Geo<BITS>::KV_PER_WAVE];
+  uint32_t kv[Geo<BITS, KG>::KV_PER_WAVE];
   uint32_t sc;
 };
 
-template <int BITS>
-__device__ __forceinline__ CopyMap<BITS> make_copy_map(int wave, int lane, int kv_heads) {
-  using G = Geo<BITS>;
-  CopyMap<BITS> cm;
+template <int BITS, int KG>
+__device__ __forceinline__ CopyMap<BITS, KG> make_copy_map(int wave, int lane, int kv_heads) {
+  using G = Geo<BITS, KG>;
+  CopyMap<BITS, KG> cm;
   const int rs = kv_heads * G::PD;
 #pragma unroll
   for (int j = 0; j < G::KV_PER_WAVE; ++j) {
@@ -129,15 +141,15 @@ __device__ __forceinline__ CopyMap<BITS> make_copy_map(int wave, int lane, int k
     cm.kv[j] = static_cast<uint32_t>(t * rs + 16 * (slot ^ phi<G::CPT>(t)));
   }
   const int pos = 64 * (wave & 3) + lane;
-  const int t = pos >> 1, slot = pos & 1;
-  cm.sc = static_cast<uint32_t>(t * kv_heads * 8 + 16 * (slot ^ phi<2>(t)));
+  const int t = pos / G::SCPT, slot = pos % G::SCPT;
+  cm.sc = static_cast<uint32_t>(t * kv_heads * 8 + 16 * (slot ^ phi<G::SCPT>(t)));
   return cm;
 }
 
-template <int BITS>
+template <int BITS, int KG>
 __device__ __forceinline__ void issue_stage(const StagedParams& p, uint32_t buf, const Cursor& c, int kvh0, int wave,
-                                            const CopyMap<BITS>& cm) {
-  using G = Geo<BITS>;
+                                            const CopyMap<BITS, KG>& cm) {
+  using G = Geo<BITS, KG>;
   const long row0 = (static_cast<long>(c.blk) * p.block_tokens + c.sb0) * p.kv_heads + kvh0;
   const uint8_t* kb = p.pk + row0 * G::PD;
   const uint8_t* vb = p.pv + row0 * G::PD;
@@ -152,13 +164,14 @@ __device__ __forceinline__ void issue_stage(const StagedParams& p, uint32_t buf,
 }
 
 // W chunk (quad, row R = 4h + g, chunk c of 8 slots) byte offset.
-template <int BITS, int QUADS>
+template <int BITS, int QUADS, int KG>
 __device__ __forceinline__ int w_chunk(int quad, int R, int c, int w, int half) {
-  if constexpr (Geo<BITS>::W_IN_K) {
+  using G = Geo<BITS, KG>;
+  if constexpr (G::W_IN_K) {
     // inside the wave's K chunks (kv head w, tokens of its half) of the stage
     const int b = c >> 2;
     const int t = kHalfTok * half + 32 * quad + (R & 7) + 8 * ((R >> 3) ^ b) + 16 * b;
-    return Geo<BITS>::K_OFF + chunk_byte<16>(t, 4 * w + (c & 3));
+    return G::K_OFF + chunk_byte<G::CPT>(t, 4 * w + (c & 3));
   } else {
     // own region after both stage buffers, [wave][quad][row][8 chunks]
     const int rp = R ^ ((R >> 2) & 1);
@@ -178,11 +191,11 @@ struct WaveState {
 // Every LDS read of the stage goes out first, the four tiles' QK chains are
 // interleaved and V is unpacked before the softmax, so the two waves of a
 // SIMD have independent work to fill each other's latencies.
-template <int BITS, int QUADS, int QSPLIT>
+template <int BITS, int QUADS, int QSPLIT, int KG>
 __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase, int hv, int w, int half, int li,
                                               int lq, const Masks& mk, const QueryOps<QUADS, QSPLIT>& qo,
                                               const u32x4 (&offa)[BITS == 4 ? 1 : 2], WaveState<BITS, QUADS>& st) {
-  using G = Geo<BITS>;
+  using G = Geo<BITS, KG>;
   constexpr int KW = BITS == 4 ? 4 : 2;   // K words per lane and tile
   constexpr int NTR = BITS == 4 ? 8 : 4;  // transpose reads (16 / 32 dims each)
   constexpr int NPAR = BITS == 4 ? 1 : 2;
@@ -193,16 +206,16 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
   for (int tau = 0; tau < 4; ++tau) {
     const int t = kHalfTok * half + 16 * tau + li;
     if (BITS == 4) {
-      const u32x4 r = *reinterpret_cast<const u32x4*>(buf + G::K_OFF + chunk_byte<16>(t, 4 * w + lq));
+      const u32x4 r = *reinterpret_cast<const u32x4*>(buf + G::K_OFF + chunk_byte<G::CPT>(t, 4 * w + lq));
 #pragma unroll
       for (int i = 0; i < KW; ++i) kraw[tau][i] = r[i];
     } else {
       const u32x2 r =
-          *reinterpret_cast<const u32x2*>(buf + G::K_OFF + chunk_byte<8>(t, 2 * w + (lq >> 1)) + 8 * (lq & 1));
+          *reinterpret_cast<const u32x2*>(buf + G::K_OFF + chunk_byte<G::CPT>(t, 2 * w + (lq >> 1)) + 8 * (lq & 1));
 #pragma unroll
       for (int i = 0; i < KW; ++i) kraw[tau][i] = r[i];
     }
-    const int sbyte = chunk_byte<2>(t, w >> 1) + 8 * (w & 1);
+    const int sbyte = chunk_byte<G::SCPT>(t, w >> 1) + 8 * (w & 1);
     skw[tau] = *reinterpret_cast<const u32x2*>(buf + G::SK_OFF + sbyte);
     svw[tau] = *reinterpret_cast<const u32x2*>(buf + G::SV_OFF + sbyte);
   }
@@ -218,8 +231,8 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
   auto read_v = [&]() {
 #pragma unroll
     for (int n = 0; n < NTR; ++n)
-      tr[n] = BITS == 4 ? lds_read_tr4(buf, G::V_OFF + chunk_byte<16>(t_tr, 4 * w + (n >> 1)) + 8 * (n & 1))
-                        : lds_read_tr4(buf, G::V_OFF + chunk_byte<8>(t_tr, 2 * w + (n >> 1)) + 8 * (n & 1));
+      tr[n] = BITS == 4 ? lds_read_tr4(buf, G::V_OFF + chunk_byte<G::CPT>(t_tr, 4 * w + (n >> 1)) + 8 * (n & 1))
+                        : lds_read_tr4(buf, G::V_OFF + chunk_byte<G::CPT>(t_tr, 2 * w + (n >> 1)) + 8 * (n & 1));
   };
   if constexpr (kEarlyV) read_v();
   // ---------------------------------------------------------------- QK
@@ -323,7 +336,7 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
     }
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int off = w_chunk<BITS, QUADS>(quad, 4 * lq + g, u >> 1, w, half) + 8 * (u & 1);
+      const int off = w_chunk<BITS, QUADS, KG>(quad, 4 * lq + g, u >> 1, w, half) + 8 * (u & 1);
       *reinterpret_cast<u32x2*>(wbase + off) = u32x2{wlo[g], whi[g]};
     }
     // rescale the PV state of column head li/4 by that head's alpha (alpha
@@ -346,7 +359,7 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
   for (int quad = 0; quad < QUADS; ++quad)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
-      wb[quad][kk] = *reinterpret_cast<const u32x4*>(wbase + w_chunk<BITS, QUADS>(quad, li, 4 * kk + lq, w, half));
+      wb[quad][kk] = *reinterpret_cast<const u32x4*>(wbase + w_chunk<BITS, QUADS, KG>(quad, li, 4 * kk + lq, w, half));
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -365,24 +378,25 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
       for (int c = 0; c < NPAR; ++c) st.corr[quad][c] = mfma16(offa[c], wb[quad][kk], st.corr[quad][c]);
 }
 
-template <int BITS, int QUADS, int QSPLIT, typename QT>
+template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
 __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p) {
-  using G = Geo<BITS>;
+  using G = Geo<BITS, KG>;
+  constexpr int kStage = kStageTok<KG>;
   constexpr int kWBytes = G::W_IN_K ? 0 : kWaves * QUADS * 2048;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * G::STAGE + kWBytes + kMaxUnits * 8];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int w = wave & (kKG - 1);
-  const int half = wave / kKG;
+  const int w = wave & (KG - 1);
+  const int half = wave / KG;
   const int li = lane & 15;
   const int lq = lane >> 4;
 
-  // workgroup -> (split, group of 4 kv heads).  Consecutive workgroup ids go
+  // workgroup -> (split, group of KG kv heads).  Consecutive workgroup ids go
   // to different XCDs (round robin over 8); every group of split s gets an id
   // with id % 8 == s % 8, so they share one XCD and its L2: the groups read
   // complementary parts of the same 128-byte lines of the scale rows.
-  const int groups = p.kv_heads / kKG;
+  const int groups = p.kv_heads / KG;
   const int xcd = blockIdx.x & 7;
   const int rest = blockIdx.x >> 3;
   const int grp = rest % groups;
@@ -390,10 +404,10 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   if (split >= p.splits) return;  // padding ids of the last round
   const int u_begin = split * p.blocks_per_split;
   const int u_end = min(p.units, u_begin + p.blocks_per_split);
-  const int kvh0 = grp * kKG;
+  const int kvh0 = grp * KG;
   const int head0 = (kvh0 + w) * p.gq;
 
-  const CopyMap<BITS> cm = make_copy_map<BITS>(wave, lane, p.kv_heads);
+  const CopyMap<BITS, KG> cm = make_copy_map<BITS, KG>(wave, lane, p.kv_heads);
   const uint32_t lds0 = lds_addr(lds);
   int* units = reinterpret_cast<int*>(lds + 2 * G::STAGE + kWBytes);
   const int n_units = max(0, u_end - u_begin);  // <= kMaxUnits, checked on the host
@@ -408,31 +422,31 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // stages in flight arrive nearly as soon as one.
   constexpr int kStageCopies = 2 * G::KV_PER_WAVE + 1;    // copy instructions per wave per stage
   constexpr int kUnitCopies = kMaxUnits / (64 * kWaves);  // dword copies per wave for the valid counts
-  constexpr int kQBytesMax = kKG * 4 * QUADS * 128 * static_cast<int>(sizeof(QT));
+  constexpr int kQBytesMax = KG * 4 * QUADS * 128 * static_cast<int>(sizeof(QT));
   constexpr bool kEarlyFits = kWaves * coop_scratch_bytes<QUADS> + kQBytesMax <= G::STAGE;
   const bool direct = kEarlyFits && p.table == nullptr && (reinterpret_cast<uintptr_t>(p.query) & 15u) == 0;
   auto advance = [&](Cursor& c) -> bool {
-    return direct ? next_stage_direct<kStageTok>(c, units, u_begin, p.block_tokens, n_units)
-                  : next_stage<kStageTok>(c, units, n_units);
+    return direct ? next_stage_direct<kStage>(c, units, u_begin, p.block_tokens, n_units)
+                  : next_stage<kStage>(c, units, n_units);
   };
 
   QueryOps<QUADS, QSPLIT> qo;
-  Cursor cur{-1, 0, 0, -kStageTok};
-  Cursor nxt{-1, 0, 0, -kStageTok};
+  Cursor cur{-1, 0, 0, -kStage};
+  Cursor nxt{-1, 0, 0, -kStage};
   bool have = false, have_n = false;
   bool pre1 = false;   // stage 1 went out early and is the loop's second stage
   bool wait0 = true;   // the loop's first pass waits for its stage and meets the barrier
-  bool spec = false;   // stage 0 (the split's first block, tokens 0..127) went out early
+  bool spec = false;   // stage 0 (the split's first block, its first stage of tokens) went out early
   if (direct) {
     uint8_t* qrows = lds + 2 * G::STAGE - kQBytesMax;  // tail of the second stage buffer
-    const int qcopies = kKG * p.gq * 128 * static_cast<int>(sizeof(QT)) / 1024;
+    const int qcopies = KG * p.gq * 128 * static_cast<int>(sizeof(QT)) / 1024;
     const uint8_t* qsrc =
         static_cast<const uint8_t*>(p.query) + static_cast<long>(kvh0) * p.gq * 128 * static_cast<long>(sizeof(QT));
     for (int i = wave; i < qcopies; i += kWaves)
       dma16<false>(qsrc, 1024u * static_cast<uint32_t>(i) + 16u * static_cast<uint32_t>(lane),
                    lds_addr(qrows) + 1024u * static_cast<uint32_t>(i));
     if (n_units > 0) {
-      issue_stage<BITS>(p, lds0, Cursor{0, u_begin, 0, 0}, kvh0, wave, cm);
+      issue_stage<BITS, KG>(p, lds0, Cursor{0, u_begin, 0, 0}, kvh0, wave, cm);
       spec = true;
     }
     const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(p.valid + (n_units > 0 ? u_begin : 0));
@@ -452,14 +466,14 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     Cursor c1{-1, 0, 0, 0};
     bool issued1 = false;
     if (spec) {
-      if (p.block_tokens > kStageTok) {
-        c1 = Cursor{0, u_begin, 0, kStageTok};
+      if (p.block_tokens > kStage) {
+        c1 = Cursor{0, u_begin, 0, kStage};
         issued1 = true;
       } else if (n_units > 1) {
         c1 = Cursor{1, u_begin + 1, 0, 0};
         issued1 = true;
       }
-      if (issued1) issue_stage<BITS>(p, lds0 + static_cast<uint32_t>(G::STAGE), c1, kvh0, wave, cm);
+      if (issued1) issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>(G::STAGE), c1, kvh0, wave, cm);
     }
     // stage 0 and the valid counts landed (stage 1 may still be in flight)
     if (issued1) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies));
@@ -471,7 +485,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
       // the first valid stage is elsewhere (empty or partial blocks): let this
       // wave's early copies land, then load the right ones
       __builtin_amdgcn_s_waitcnt(0x0F70);
-      issue_stage<BITS>(p, lds0, cur, kvh0, wave, cm);
+      issue_stage<BITS, KG>(p, lds0, cur, kvh0, wave, cm);
       wait0 = true;
     }
     nxt = cur;
@@ -480,12 +494,12 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     if (issued1 && !pre1) wait0 = true;  // the early stage 1 must land before its buffer is reloaded
   } else {
     // The first stage's copies go out before anything else: the split's first
-    // attended block, tokens 0..127 (one scalar read with a block table).  If
-    // that block holds no valid token they are simply not used.
+    // attended block, its first stage of tokens (one scalar read with a block
+    // table).  If that block holds no valid token they are simply not used.
     if (u_begin < u_end) {
       Cursor c0{0, __builtin_amdgcn_readfirstlane(p.table ? p.table[u_begin] : u_begin), 0, 0};
       if (c0.blk >= 0 && c0.blk < p.num_blocks) {
-        issue_stage<BITS>(p, lds0, c0, kvh0, wave, cm);
+        issue_stage<BITS, KG>(p, lds0, c0, kvh0, wave, cm);
         spec = true;
       }
     }
@@ -502,7 +516,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     have = advance(cur);
     if (have && !(spec && cur.u == 0 && cur.sb0 == 0)) {
       __builtin_amdgcn_s_waitcnt(0x0F70);
-      issue_stage<BITS>(p, lds0, cur, kvh0, wave, cm);
+      issue_stage<BITS, KG>(p, lds0, cur, kvh0, wave, cm);
     }
     // query operands, through per-wave scratch in the second stage buffer (its
     // first copies go out after the loop's first barrier)
@@ -544,13 +558,13 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
       __syncthreads();                     // ... everyone's; and the other buffer is free
     }
     if (have_n && !(first && pre1))
-      issue_stage<BITS>(p, lds0 + static_cast<uint32_t>((buf ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
+      issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>((buf ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
     first = false;
-    const int hv = min(kStageTok, cur.vb - cur.sb0) - kHalfTok * half;
+    const int hv = min(kStage, cur.vb - cur.sb0) - kHalfTok * half;
     if (hv > 0) {
       uint8_t* sbuf = lds + buf * G::STAGE;
       uint8_t* wbase = G::W_IN_K ? sbuf : lds + 2 * G::STAGE + wave * QUADS * 2048;
-      compute_stage<BITS, QUADS, QSPLIT>(sbuf, wbase, hv, w, half, li, lq, mk, qo, offa, st);
+      compute_stage<BITS, QUADS, QSPLIT, KG>(sbuf, wbase, hv, w, half, li, lq, mk, qo, offa, st);
     }
     cur = nxt;
     have = have_n;
@@ -562,9 +576,9 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // out = F (C - corr) per column: F = 64 (INT2 parity 0: 4, parity 1: 16)
   // lane (li, lq): column (head li/4, group li%4), rows = dims of its tiles
   float* xo = reinterpret_cast<float*>(lds);  // [w][quad][lane][8] from half 1
-  float* xm = xo + kKG * QUADS * 64 * 8;      // [w][quad][4 heads][2]
+  float* xm = xo + KG * QUADS * 64 * 8;       // [w][quad][4 heads][2]
   __builtin_amdgcn_s_waitcnt(0x0F70);  // no copy of this wave is still writing LDS
-  __syncthreads();                     // every wave is done with the stage buffers
+  if constexpr (G::HALVES == 2) __syncthreads();  // every wave is done with the stage buffers
   float ov[QUADS][8];
   float mh[QUADS], lh[QUADS];
 #pragma unroll
@@ -594,7 +608,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     const float l_tot = row_sum16(st.l_run[quad]);
     mh[quad] = __shfl(st.m_run[quad], (li >> 2) << 4, kWave);
     lh[quad] = __shfl(l_tot, (li >> 2) << 4, kWave);
-    if (half == 1) {
+    if (G::HALVES == 2 && half == 1) {
       float* dst = xo + ((w * QUADS + quad) * 64 + lane) * 8;
 #pragma unroll
       for (int i = 0; i < 8; ++i) dst[i] = ov[quad][i];
@@ -604,14 +618,17 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
       }
     }
   }
-  __syncthreads();
-  if (half == 1) return;
+  if constexpr (G::HALVES == 2) {
+    __syncthreads();
+    if (half == 1) return;
+  }
   const long prow = static_cast<long>(split) * p.query_heads + head0;
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
+    // the other half's state (none with one half per stage)
     const float* src = xo + ((w * QUADS + quad) * 64 + lane) * 8;
-    const float mb = xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2];
-    const float lb = xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2 + 1];
+    const float mb = G::HALVES == 2 ? xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2] : -INFINITY;
+    const float lb = G::HALVES == 2 ? xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2 + 1] : 0.0f;
     const float ma = mh[quad], la = lh[quad];
     const float mm = fmaxf(ma, mb);
     const float wa = (la > 0.0f) ? exp2f(ma - mm) : 0.0f;
@@ -624,8 +641,12 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
       f32x4 o0, o1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        o0[i] = (wa != 0.0f ? wa * ov[quad][i] : 0.0f) + (wb2 != 0.0f ? wb2 * src[i] : 0.0f);
-        o1[i] = (wa != 0.0f ? wa * ov[quad][4 + i] : 0.0f) + (wb2 != 0.0f ? wb2 * src[4 + i] : 0.0f);
+        o0[i] = wa != 0.0f ? wa * ov[quad][i] : 0.0f;
+        o1[i] = wa != 0.0f ? wa * ov[quad][4 + i] : 0.0f;
+        if (G::HALVES == 2) {
+          o0[i] += wb2 != 0.0f ? wb2 * src[i] : 0.0f;
+          o1[i] += wb2 != 0.0f ? wb2 * src[4 + i] : 0.0f;
+        }
       }
       if (BITS == 4) {
         // tiles 2g, 2g+1: dims 16n + 4lq + i
@@ -647,25 +668,25 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   }
 }
 
-template <int BITS, int QUADS, int QSPLIT, typename QT>
+template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
 void launch_one(const StagedParams& prm, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((decode_staged_kernel<BITS, QUADS, QSPLIT, QT>), dim3(grid), dim3(kThreads), 0, s, prm);
+  hipLaunchKernelGGL((decode_staged_kernel<BITS, QUADS, QSPLIT, QT, KG>), dim3(grid), dim3(kThreads), 0, s, prm);
 }
 
-template <int BITS, int QUADS>
+template <int BITS, int QUADS, int KG>
 int launch_quads(const StagedParams& prm, int grid, int dtype, hipStream_t s) {
   switch (dtype) {
     case KVSSD_DTYPE_F16:
-      launch_one<BITS, QUADS, 1, _Float16>(prm, grid, s);
+      launch_one<BITS, QUADS, 1, _Float16, KG>(prm, grid, s);
       break;
     case KVSSD_DTYPE_BF16:
-      launch_one<BITS, QUADS, 2, uint16_t>(prm, grid, s);
+      launch_one<BITS, QUADS, 2, uint16_t, KG>(prm, grid, s);
       break;
     case KVSSD_DTYPE_F32:
-      launch_one<BITS, QUADS, 2, float>(prm, grid, s);
+      launch_one<BITS, QUADS, 2, float, KG>(prm, grid, s);
       break;
     case KVSSD_DTYPE_F64:
-      launch_one<BITS, QUADS, 2, double>(prm, grid, s);
+      launch_one<BITS, QUADS, 2, double, KG>(prm, grid, s);
       break;
     default:
       return arg_error("unsupported query dtype");
@@ -673,7 +694,24 @@ int launch_quads(const StagedParams& prm, int grid, int dtype, hipStream_t s) {
   return hip_status(hipGetLastError(), "decode_staged launch");
 }
 
+template <int KG>
+int launch_kg(const StagedParams& prm, int bits, int dtype, hipStream_t s) {
+  const int grid = 8 * (prm.kv_heads / KG) * ((prm.splits + 7) / 8);
+  const bool two = prm.gq > 4;
+  if (bits == 4) return two ? launch_quads<4, 2, KG>(prm, grid, dtype, s) : launch_quads<4, 1, KG>(prm, grid, dtype, s);
+  return two ? launch_quads<2, 2, KG>(prm, grid, dtype, s) : launch_quads<2, 1, KG>(prm, grid, dtype, s);
+}
+
 }  // namespace
+
+bool staged_wide(const kvssd_decode_desc& d, int units) {
+  // all 8 kv heads of a row per workgroup once the context gives every
+  // workgroup at least one block: 2048 (kv head, split) work items, 256
+  // workgroups
+  const int gq = d.kv_heads > 0 ? d.query_heads / d.kv_heads : 0;
+  return d.head_dim == 128 && d.group_size == 32 && (d.bits == 2 || d.bits == 4) && d.kv_heads % 8 == 0 &&
+         d.block_tokens % 128 == 0 && gq >= 1 && gq <= 8 && static_cast<long>(units) * d.kv_heads >= 2048;
+}
 
 bool staged_supported(const kvssd_decode_desc& d, std::string* why) {
   auto no = [&](const char* r) {
@@ -682,8 +720,8 @@ bool staged_supported(const kvssd_decode_desc& d, std::string* why) {
   };
   if (d.head_dim != 128) return no("head_dim must be 128");
   if (d.group_size != 32) return no("group_size must be 32");
-  if (d.block_tokens % kStageTok) return no("block_tokens must be a multiple of 128");
-  if (d.kv_heads % kKG) return no("kv_heads must be a multiple of 4");
+  if (d.block_tokens % 128) return no("block_tokens must be a multiple of 128");
+  if (d.kv_heads % 4) return no("kv_heads must be a multiple of 4");
   const int units = d.num_selected > 0 ? d.num_selected : d.num_blocks;
   if (plan_splits(d, units).blocks_per_split > kMaxUnits) return no("too many blocks per split");
   const int gq = d.query_heads / d.kv_heads;
@@ -717,12 +755,8 @@ int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials part
   prm.blocks_per_split = plan.blocks_per_split;
   prm.gq = d.query_heads / d.kv_heads;
   prm.scale_log2 = static_cast<float>(d.sm_scale) * kLog2e;
-  const int grid = 8 * (d.kv_heads / kKG) * ((plan.splits + 7) / 8);
-  const bool two = prm.gq > 4;
-  if (d.bits == 4) return two ? launch_quads<4, 2>(prm, grid, d.query_dtype, a.stream)
-                              : launch_quads<4, 1>(prm, grid, d.query_dtype, a.stream);
-  return two ? launch_quads<2, 2>(prm, grid, d.query_dtype, a.stream)
-             : launch_quads<2, 1>(prm, grid, d.query_dtype, a.stream);
+  if (staged_wide(d, a.units)) return launch_kg<8>(prm, d.bits, d.query_dtype, a.stream);
+  return launch_kg<4>(prm, d.bits, d.query_dtype, a.stream);
 }
 
 }  // namespace kvssd

@@ -20,13 +20,15 @@ namespace {
 constexpr int kMergeThreads = 256;
 constexpr int kMaxMergeSplits = 2048;
 
-// One workgroup per (query head, 32-dim slice); thread (phase, dim) owns the
-// splits s = phase (mod 8) of one dim.  Its first 16 O loads go out together
-// with the workgroup's load of every split's (m, l), so the common case
-// (<= 128 splits) costs one round trip to memory; the split weights
-// 2^(m_s - M) are formed once, in LDS, and the 8 phases meet in LDS at the end.
-constexpr int kSliceDims = 32;
-constexpr int kPhases = kMergeThreads / kSliceDims;  // 8
+// One workgroup per (query head, 16-dim slice): 8 per head of 128 dims, so a
+// 32-head decode spreads over 256 workgroups (every CU pulls a share of the
+// partials).  Thread (phase, dim) owns the splits s = phase (mod 16) of one
+// dim.  Its first 16 O loads go out together with the workgroup's load of
+// every split's (m, l), so the common case (<= 256 splits) costs one round
+// trip to memory; the split weights 2^(m_s - M) are formed once, in LDS, and
+// the 16 phases meet in LDS at the end.
+constexpr int kSliceDims = 16;
+constexpr int kPhases = kMergeThreads / kSliceDims;  // 16
 constexpr int kBatch = 16;
 
 __global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(const float* __restrict__ part_o,

@@ -320,3 +320,33 @@ def test_many_blocks_with_empty_and_partial_split_starts(cuda_device, bits):
         for kernel in names:
             out, lse = HipAttentionBackend(kernel).run(query, batch, 0.1)
             check(out, lse, ref_out, ref_lse)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize(("qh", "kvh"), [(8, 8), (32, 8), (64, 8), (48, 16)])
+def test_staged_eight_kv_heads_per_workgroup(cuda_device, bits, qh, kvh):
+    # kv_heads % 8 == 0 and at least 2048 (kv head, attended block) pairs: the
+    # staged kernel gives each workgroup all 8 kv heads of a token row in
+    # 64-token stages.  Empty blocks and valid counts inside the first stage
+    # sit at split starts; the same blocks are then attended through a
+    # scattered block table.
+    rng = np.random.default_rng(1000 * bits + qh + kvh)
+    nb = 2048 // kvh + 64
+    q, pk, pv, sk, sv, _ = make_batch(7 + kvh, qh, kvh, 128, nb, 128, bits, 32)
+    valid = rng.integers(1, 129, nb).astype(np.int32)
+    valid[::4] = 0
+    valid[1::8] = rng.integers(0, 3, nb // 8)
+    valid[2::16] = rng.integers(60, 70, nb // 16)
+    valid[-3:] = 0
+    ids = [int(i) for i in rng.permutation(nb)[: 2048 // kvh + 40]]
+    table = np.array(ids, np.int32)
+    for qdtype in (torch.float32, torch.float16, torch.bfloat16):
+        qq = torch.from_numpy(q).to(qdtype).float().numpy()
+        query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, qdtype=qdtype)
+        assert HipAttentionBackend("auto").kernel_for(query, batch) == "staged"
+        for selection in (None, ids):
+            ref_out, ref_lse = O.attention(
+                qq, pk, pv, sk, sv, valid, bits, 32, 0.1, block_table=None if selection is None else table, threads=16
+            )
+            out, lse = HipAttentionBackend("staged").run(query, batch, 0.1, block_table=selection)
+            check(out, lse, ref_out, ref_lse)
