@@ -337,9 +337,15 @@ __device__ __forceinline__ QueryRaw<QUADS> coop_query_load(const void* query, in
     const int hq = quad * 4 + h;
     const bool have = hq < gq;
     const int base = (head0 + (have ? hq : 0)) * 128;
+    // every load is issued (the head is clamped into range) and masked
+    // afterwards: a load under a lane condition becomes a branch with a wait
+    // for all outstanding memory operations at its end -- including the stage
+    // copies already in flight
 #pragma unroll
-    for (int sl = 0; sl < 8; ++sl)
-      r.x[quad][sl] = have ? load_query<QT>(query, base + qk_dim<BITS>(m, q, sl)) : 0.0f;
+    for (int sl = 0; sl < 8; ++sl) {
+      const float v = load_query<QT>(query, base + qk_dim<BITS>(m, q, sl));
+      r.x[quad][sl] = have ? v : 0.0f;
+    }
   }
   return r;
 }
