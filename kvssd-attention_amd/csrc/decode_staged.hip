@@ -416,12 +416,11 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // second stage buffer for the query scratch and the workgroup's query
   // rows): every early memory operation is an LDS copy, so no compiler-placed
   // wait for a load can also wait for a stage.  The query rows go first, then
-  // stage 0 and the split's valid counts; once the rows land the query
-  // operands are built and stage 1 goes out (~2 us after entry instead of
-  // after stage 0 has landed, ~6 us): the start is latency-bound, and two
-  // stages in flight arrive nearly as soon as one.
+  // the split's valid counts (one copy per 64 units) and stage 0; once the
+  // rows and counts land the query operands are built and stage 1 goes out,
+  // before stage 0 has landed: the start is latency-bound, and two stages in
+  // flight arrive nearly as soon as one.
   constexpr int kStageCopies = 2 * G::KV_PER_WAVE + 1;    // copy instructions per wave per stage
-  constexpr int kUnitCopies = kMaxUnits / (64 * kWaves);  // dword copies per wave for the valid counts
   constexpr int kQBytesMax = KG * 4 * QUADS * 128 * static_cast<int>(sizeof(QT));
   constexpr bool kEarlyFits = kWaves * coop_scratch_bytes<QUADS> + kQBytesMax <= G::STAGE;
   const bool direct = kEarlyFits && p.table == nullptr && (reinterpret_cast<uintptr_t>(p.query) & 15u) == 0;
@@ -445,20 +444,20 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     for (int i = wave; i < qcopies; i += kWaves)
       dma16<false>(qsrc, 1024u * static_cast<uint32_t>(i) + 16u * static_cast<uint32_t>(lane),
                    lds_addr(qrows) + 1024u * static_cast<uint32_t>(i));
+    // the split's valid counts, 64 per copy (lanes past the end re-read the last one)
+    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(p.valid + (n_units > 0 ? u_begin : 0));
+    const int ulast = max(n_units - 1, 0);
+    for (int i0 = 64 * wave; i0 < n_units; i0 += 64 * kWaves)
+      dma4(vsrc, 4u * static_cast<uint32_t>(min(i0 + lane, ulast)),
+           lds_addr(reinterpret_cast<const uint8_t*>(units)) + 4u * static_cast<uint32_t>(i0));
     if (n_units > 0) {
       issue_stage<BITS, KG>(p, lds0, Cursor{0, u_begin, 0, 0}, kvh0, wave, cm);
       spec = true;
     }
-    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(p.valid + (n_units > 0 ? u_begin : 0));
-    const int ulast = max(n_units - 1, 0);
-#pragma unroll
-    for (int j = 0; j < kUnitCopies; ++j) {
-      const int i0 = (j * kWaves + wave) * 64;
-      dma4(vsrc, 4u * static_cast<uint32_t>(min(i0 + lane, ulast)), lds_addr(reinterpret_cast<const uint8_t*>(units)) + 4u * static_cast<uint32_t>(i0));
-    }
-    // the query rows (issued first) have landed once at most the later copies are outstanding
-    if (spec) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies + kUnitCopies));
-    else __builtin_amdgcn_s_waitcnt(vmcnt_wait(kUnitCopies));
+    // the query rows and the valid counts (issued first) have landed once at
+    // most the stage's copies are outstanding (copies complete in issue order)
+    if (spec) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies));
+    else __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     coop_query_build<BITS, QUADS, QSPLIT>(qo, coop_query_load<BITS, QUADS, QT>(qrows, p.gq, w * p.gq, lane),
                                           p.scale_log2, lane, lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
