@@ -14,8 +14,8 @@ Output: one JSON line.  ``value`` is packed-KV GB/s over the whole step
 only at the two ends, after W untimed steps: 2000 by default, ~70 ms of load,
 since the GPU needs tens of milliseconds of work to reach its steady clocks
 and a short warmup reads ~8% slow); ``roofline.achieved`` is the same bytes over the
-dominant (split) kernel's average duration, from HIP events recorded on the
-launch stream right around that kernel in a second pass over the same steps.
+dominant (split) kernel's average duration: a second pass launches the split
+kernel alone K times back to back between two HIP events on its stream.
 ``cpu_baseline`` is the CPU oracle (a plain-C port of the reference's
 dequantise-then-attend path) timed on this host's cores over a bounded sample
 of the same workload.
@@ -530,9 +530,6 @@ def main() -> int:
             work.data_ptr(), work.numel(), sh,
         )
 
-    def merge():
-        return lib.kvssd_hip_decode_merge(ctypes.byref(desc), work.data_ptr(), work.numel(), out.data_ptr(), lse.data_ptr(), sh)
-
     def step(i: int):
         # one decode through the entry point the backend and the stager call
         b = batches[i % copies]
@@ -559,24 +556,20 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = start.elapsed_time(end) / args.steps
-    # second pass: the split kernel's own duration, from events recorded on the
-    # launch stream right around it (an event record costs a few microseconds
-    # of stream time, so this pass is not the step timing)
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    # second pass: the split kernel alone, the same K launches back to back
+    # between two events on the launch stream: its average duration (plus the
+    # dispatch gap between back-to-back launches, ~0.5 us, which rocprof's
+    # per-dispatch durations leave out)
+    k_start = torch.cuda.Event(enable_timing=True)
+    k_end = torch.cuda.Event(enable_timing=True)
+    k_start.record(stream)
     for i in range(args.steps):
-        evs[i][0].record(stream)
         rc = partials(i)
-        evs[i][1].record(stream)
-        rc = rc or merge()
         if rc:
-            _native.check(rc, "decode")
+            _native.check(rc, "decode_partials")
+    k_end.record(stream)
     torch.cuda.synchronize()
-    kern_ms = [a.elapsed_time(b) for a, b in evs]
-    kern_avg = sum(kern_ms) / len(kern_ms)
-
-    def pct(xs, p):
-        s = sorted(xs)
-        return s[min(len(s) - 1, int(p * len(s)))]
+    kern_avg = k_start.elapsed_time(k_end) / args.steps
 
     gbps = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (kern_avg * 1e-3) / 1e9
@@ -619,7 +612,7 @@ def main() -> int:
             "kv_copies_rotated": copies,
             "alg_bytes_per_step": nbytes,
         },
-        "kernel_us": {"avg": round(kern_avg * 1e3, 2), "p10": round(pct(kern_ms, 0.1) * 1e3, 2), "p50": round(pct(kern_ms, 0.5) * 1e3, 2), "p90": round(pct(kern_ms, 0.9) * 1e3, 2)},
+        "kernel_us": {"avg": round(kern_avg * 1e3, 2), "timing": "K split launches back to back between two events"},
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
