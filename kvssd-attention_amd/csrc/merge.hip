@@ -17,95 +17,98 @@
 namespace kvssd {
 namespace {
 
-constexpr int kMergeThreads = 256;
+constexpr int kMergeThreads = 256;  // merge_chunks
 constexpr int kMaxMergeSplits = 2048;
 
-// One workgroup per (query head, 16-dim slice): 8 per head of 128 dims, so a
-// 32-head decode spreads over 256 workgroups (every CU pulls a share of the
-// partials).  Thread (phase, dim) owns the splits s = phase (mod 16) of one
-// dim.  Its first 16 O loads go out together with the workgroup's load of
-// every split's (m, l), so the common case (<= 256 splits) costs one round
-// trip to memory; the split weights 2^(m_s - M) are formed once, in LDS, and
-// the 16 phases meet in LDS at the end.
+// One single-wave workgroup per (query head, 16-dim slice): a 32-head decode
+// spreads over 256 waves, so every CU pulls a share of the partials.  Splits
+// go in batches of 4 OPL (OPL = 64, or 16 when there are at most 64 splits).
+// Lane (phase, dim) = (lane / 16, lane % 16) owns the O values of splits
+// s = phase (mod 4) of one dim (OPL per batch); lane L owns the (m, l) of
+// splits s = L (mod 64) (OPL / 16 per batch).  Every load of a
+// batch goes out at once (indices clamped into range, so that no load sits
+// under a branch; 32-bit offsets from the uniform base, so that 64 loads in
+// flight fit the registers): up to 4 OPL splits cost one round trip to memory.
+// The batch max and L are wave reductions; the weights 2^(m_s - M) go
+// through a per-wave LDS table laid out [phase][j] so that each lane reads
+// its 64 weights with 16 vector reads (one wave writes and reads it: LDS
+// keeps the order, no barrier).  A later batch rescales the running
+// (M, L, O) exactly.
 constexpr int kSliceDims = 16;
-constexpr int kPhases = kMergeThreads / kSliceDims;  // 16
-constexpr int kBatch = 16;
+constexpr int kPhases = kWave / kSliceDims;  // 4
 
-__global__ __launch_bounds__(kMergeThreads) void merge_splits_kernel(const float* __restrict__ part_o,
-                                                                     const float* __restrict__ part_ml, int splits,
-                                                                     int query_heads, int head_dim,
-                                                                     float* __restrict__ out, float* __restrict__ lse) {
-  __shared__ float sw[kMaxMergeSplits];  // m_s, then the weight 2^(m_s - M) (0 for empty splits)
-  __shared__ float sl[kMaxMergeSplits];
-  __shared__ float red[kMergeThreads / kWave];
-  __shared__ float partial[kPhases][kSliceDims];
+template <int OPL>
+__global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __restrict__ part_o,
+                                                            const float* __restrict__ part_ml, int splits,
+                                                            int query_heads, int head_dim, float* __restrict__ out,
+                                                            float* __restrict__ lse) {
+  constexpr int kBatchSplits = kPhases * OPL;
+  constexpr int kOPerLane = OPL;
+  constexpr int kMlPerLane = kBatchSplits / kWave;
+  __shared__ float sw[kBatchSplits];  // [phase][j]: weight of split phase + 4 j of the batch
   const int h = blockIdx.x;
   const int d0 = blockIdx.y * kSliceDims;
-  const int tid = threadIdx.x;
-  const int dd = tid % kSliceDims;
-  const int ph = tid / kSliceDims;
+  const int lane = threadIdx.x;
+  const int ph = lane / kSliceDims;
+  const int dd = lane % kSliceDims;
   const bool live = d0 + dd < head_dim;
-  const int dcol = live ? d0 + dd : d0;
-
-  float ov[kBatch];
+  const uint32_t dcol = static_cast<uint32_t>(live ? d0 + dd : d0);
+  const uint8_t* ob = reinterpret_cast<const uint8_t*>(part_o);
+  const uint8_t* mb = reinterpret_cast<const uint8_t*>(part_ml);
+  const uint32_t qh = static_cast<uint32_t>(query_heads), hd = static_cast<uint32_t>(head_dim);
+  float big_m = -INFINITY, big_l = 0.0f, acc = 0.0f;
+  for (int base = 0; base < splits; base += kBatchSplits) {
+    float ov[kOPerLane];
 #pragma unroll
-  for (int j = 0; j < kBatch; ++j) {
-    const int s = ph + kPhases * j;
-    ov[j] = s < splits ? part_o[(static_cast<long>(s) * query_heads + h) * head_dim + dcol] : 0.0f;
-  }
-  float mx = -INFINITY;
-  for (int s = tid; s < splits; s += kMergeThreads) {
-    const long r = static_cast<long>(s) * query_heads + h;
-    const float m = part_ml[2 * r], l = part_ml[2 * r + 1];
-    sw[s] = m;
-    sl[s] = l;
-    if (l > 0.0f) mx = fmaxf(mx, m);
-  }
-  // M = max over non-empty splits
-  mx = wave_max(mx);
-  if (tid % kWave == 0) red[tid / kWave] = mx;
-  __syncthreads();
-  float big_m = red[0];
-#pragma unroll
-  for (int w = 1; w < kMergeThreads / kWave; ++w) big_m = fmaxf(big_m, red[w]);
-  // weights and L = sum_s w_s l_s
-  float lsum = 0.0f;
-  for (int s = tid; s < splits; s += kMergeThreads) {
-    const float l = sl[s];
-    const float w = l > 0.0f ? exp2f(sw[s] - big_m) : 0.0f;
-    sw[s] = w;
-    lsum += w * l;
-  }
-  lsum = wave_sum(lsum);
-  __syncthreads();  // every lane has read red[] before it is reused
-  if (tid % kWave == 0) red[tid / kWave] = lsum;
-  __syncthreads();  // weights and partial sums visible
-  float big_l = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kMergeThreads / kWave; ++w) big_l += red[w];
-
-  float acc = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kBatch; ++j) {
-    const int s = ph + kPhases * j;
-    if (s < splits) {
-      const float w = sw[s];
-      if (w != 0.0f) acc += w * ov[j];
+    for (int j = 0; j < kOPerLane; ++j) {
+      const int s = min(base + ph + kPhases * j, splits - 1);
+      const uint32_t r = static_cast<uint32_t>(s) * qh + static_cast<uint32_t>(h);
+      ov[j] = *reinterpret_cast<const float*>(ob + 4u * (r * hd + dcol));
     }
-  }
-  for (int s = ph + kPhases * kBatch; s < splits; s += kPhases) {
-    const float w = sw[s];
-    if (w != 0.0f) acc += w * part_o[(static_cast<long>(s) * query_heads + h) * head_dim + dcol];
-  }
-  partial[ph][dd] = acc;
-  __syncthreads();
-  if (ph == 0) {
-    float sum = 0.0f;
+    float mv[kMlPerLane], lv[kMlPerLane];
 #pragma unroll
-    for (int q = 0; q < kPhases; ++q) sum += partial[q][dd];
-    if (live) out[static_cast<long>(h) * head_dim + d0 + dd] = big_l > 0.0f ? sum / big_l : 0.0f;
-    if (dd == 0 && blockIdx.y == 0) lse[h] = big_l > 0.0f ? kLn2 * (big_m + log2f(big_l)) : -INFINITY;
+    for (int k = 0; k < kMlPerLane; ++k) {
+      const int s = base + lane + kWave * k;
+      const uint32_t r = static_cast<uint32_t>(min(s, splits - 1)) * qh + static_cast<uint32_t>(h);
+      const float2 ml = *reinterpret_cast<const float2*>(mb + 8u * r);
+      mv[k] = ml.x;
+      lv[k] = s < splits ? ml.y : 0.0f;
+    }
+    // M over the non-empty splits seen so far
+    float bm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kMlPerLane; ++k) bm = lv[k] > 0.0f ? fmaxf(bm, mv[k]) : bm;
+    // (no branch on an empty batch: the O loads must not sink below one; with
+    // M = -inf every weight is 0 through the l > 0 guard)
+    const float m_new = fmaxf(big_m, wave_max(bm));
+    float lsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMlPerLane; ++k) {
+      const float w = lv[k] > 0.0f ? exp2f(mv[k] - m_new) : 0.0f;
+      lsum += w * lv[k];
+      const int sb = lane + kWave * k;  // split of the batch
+      sw[(sb % kPhases) * kOPerLane + sb / kPhases] = w;
+    }
+    lsum = wave_sum(lsum);
+    float osum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kOPerLane; j += 4) {
+      const float4 w4 = *reinterpret_cast<const float4*>(&sw[ph * kOPerLane + j]);
+      osum += w4.x != 0.0f ? w4.x * ov[j] : 0.0f;
+      osum += w4.y != 0.0f ? w4.y * ov[j + 1] : 0.0f;
+      osum += w4.z != 0.0f ? w4.z * ov[j + 2] : 0.0f;
+      osum += w4.w != 0.0f ? w4.w * ov[j + 3] : 0.0f;
+    }
+    // sum over the 4 phases: lanes dd, dd + 16, dd + 32, dd + 48
+    osum += __shfl_xor(osum, 16, kWave);
+    osum += __shfl_xor(osum, 32, kWave);
+    const float rescale = big_l > 0.0f ? exp2f(big_m - m_new) : 0.0f;
+    big_l = big_l * rescale + lsum;
+    acc = (rescale != 0.0f ? acc * rescale : 0.0f) + osum;
+    big_m = m_new;
   }
+  if (ph == 0 && live) out[static_cast<long>(h) * head_dim + d0 + dd] = big_l > 0.0f ? acc / big_l : 0.0f;
+  if (lane == 0 && blockIdx.y == 0) lse[h] = big_l > 0.0f ? kLn2 * (big_m + log2f(big_l)) : -INFINITY;
 }
 
 __global__ __launch_bounds__(kMergeThreads) void merge_chunks_kernel(int dim, float* __restrict__ acc_out,
@@ -140,8 +143,12 @@ int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int he
                         hipStream_t stream) {
   if (splits > kMaxMergeSplits) return arg_error("too many splits for the merge kernel");
   const int slices = (head_dim + kSliceDims - 1) / kSliceDims;
-  hipLaunchKernelGGL(merge_splits_kernel, dim3(query_heads, slices), dim3(kMergeThreads), 0, stream, parts.o,
-                     parts.ml, splits, query_heads, head_dim, out, lse);
+  if (splits <= kPhases * 16)
+    hipLaunchKernelGGL(merge_splits_kernel<16>, dim3(query_heads, slices), dim3(kWave), 0, stream, parts.o, parts.ml,
+                       splits, query_heads, head_dim, out, lse);
+  else
+    hipLaunchKernelGGL(merge_splits_kernel<64>, dim3(query_heads, slices), dim3(kWave), 0, stream, parts.o, parts.ml,
+                       splits, query_heads, head_dim, out, lse);
   return hip_status(hipGetLastError(), "merge_splits launch");
 }
 

@@ -350,3 +350,24 @@ def test_staged_eight_kv_heads_per_workgroup(cuda_device, bits, qh, kvh):
             )
             out, lse = HipAttentionBackend("staged").run(query, batch, 0.1, block_table=selection)
             check(out, lse, ref_out, ref_lse)
+
+
+def test_merge_of_more_than_256_splits(cuda_device):
+    # one kv head and 600 blocks: 600 splits, merged in batches of 256 with a
+    # running rescale; the first 300 blocks (a whole batch and then some) hold
+    # no valid token, and valid counts vary after that
+    rng = np.random.default_rng(77)
+    nb = 600
+    q, pk, pv, sk, sv, _ = make_batch(9, 4, 1, 128, nb, 16, 4, 32)
+    valid = rng.integers(0, 17, nb).astype(np.int32)
+    valid[:300] = 0
+    ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.2, threads=16)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, 4, 32)
+    for kernel in kernels_for(query, batch):
+        out, lse = HipAttentionBackend(kernel).run(query, batch, 0.2)
+        check(out, lse, ref_out, ref_lse)
+    # every block empty: out 0, lse -inf
+    empty = np.zeros(nb, np.int32)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, empty, 4, 32)
+    out, lse = HipAttentionBackend("auto").run(query, batch, 0.2)
+    assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
