@@ -28,7 +28,8 @@ constexpr int kMaxMergeSplits = 2048;
 // splits s = L (mod 64) (OPL / 16 per batch).  Every load of a
 // batch goes out at once (indices clamped into range, so that no load sits
 // under a branch; 32-bit offsets from the uniform base, so that 64 loads in
-// flight fit the registers): up to 4 OPL splits cost one round trip to memory.
+// flight fit the registers -- 64-bit ones, OFF = uint64_t, only for partials
+// beyond 4 GiB): up to 4 OPL splits cost one round trip to memory.
 // The batch max and L are wave reductions; the weights 2^(m_s - M) go
 // through a per-wave LDS table laid out [phase][j] so that each lane reads
 // its 64 weights with 16 vector reads (one wave writes and reads it: LDS
@@ -37,7 +38,7 @@ constexpr int kMaxMergeSplits = 2048;
 constexpr int kSliceDims = 16;
 constexpr int kPhases = kWave / kSliceDims;  // 4
 
-template <int OPL>
+template <int OPL, typename OFF>
 __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __restrict__ part_o,
                                                             const float* __restrict__ part_ml, int splits,
                                                             int query_heads, int head_dim, float* __restrict__ out,
@@ -52,24 +53,24 @@ __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __rest
   const int ph = lane / kSliceDims;
   const int dd = lane % kSliceDims;
   const bool live = d0 + dd < head_dim;
-  const uint32_t dcol = static_cast<uint32_t>(live ? d0 + dd : d0);
+  const OFF dcol = static_cast<OFF>(live ? d0 + dd : d0);
   const uint8_t* ob = reinterpret_cast<const uint8_t*>(part_o);
   const uint8_t* mb = reinterpret_cast<const uint8_t*>(part_ml);
-  const uint32_t qh = static_cast<uint32_t>(query_heads), hd = static_cast<uint32_t>(head_dim);
+  const OFF qh = static_cast<OFF>(query_heads), hd = static_cast<OFF>(head_dim);
   float big_m = -INFINITY, big_l = 0.0f, acc = 0.0f;
   for (int base = 0; base < splits; base += kBatchSplits) {
     float ov[kOPerLane];
 #pragma unroll
     for (int j = 0; j < kOPerLane; ++j) {
       const int s = min(base + ph + kPhases * j, splits - 1);
-      const uint32_t r = static_cast<uint32_t>(s) * qh + static_cast<uint32_t>(h);
+      const OFF r = static_cast<OFF>(s) * qh + static_cast<OFF>(h);
       ov[j] = *reinterpret_cast<const float*>(ob + 4u * (r * hd + dcol));
     }
     float mv[kMlPerLane], lv[kMlPerLane];
 #pragma unroll
     for (int k = 0; k < kMlPerLane; ++k) {
       const int s = base + lane + kWave * k;
-      const uint32_t r = static_cast<uint32_t>(min(s, splits - 1)) * qh + static_cast<uint32_t>(h);
+      const OFF r = static_cast<OFF>(min(s, splits - 1)) * qh + static_cast<OFF>(h);
       const float2 ml = *reinterpret_cast<const float2*>(mb + 8u * r);
       mv[k] = ml.x;
       lv[k] = s < splits ? ml.y : 0.0f;
@@ -143,12 +144,16 @@ int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int he
                         hipStream_t stream) {
   if (splits > kMaxMergeSplits) return arg_error("too many splits for the merge kernel");
   const int slices = (head_dim + kSliceDims - 1) / kSliceDims;
-  if (splits <= kPhases * 16)
-    hipLaunchKernelGGL(merge_splits_kernel<16>, dim3(query_heads, slices), dim3(kWave), 0, stream, parts.o, parts.ml,
-                       splits, query_heads, head_dim, out, lse);
+  const dim3 grid(query_heads, slices);
+  if (split_partial_bytes(splits, query_heads, head_dim) > 0xFFFFFFFFull)
+    hipLaunchKernelGGL((merge_splits_kernel<16, uint64_t>), grid, dim3(kWave), 0, stream, parts.o, parts.ml, splits,
+                       query_heads, head_dim, out, lse);
+  else if (splits <= kPhases * 16)
+    hipLaunchKernelGGL((merge_splits_kernel<16, uint32_t>), grid, dim3(kWave), 0, stream, parts.o, parts.ml, splits,
+                       query_heads, head_dim, out, lse);
   else
-    hipLaunchKernelGGL(merge_splits_kernel<64>, dim3(query_heads, slices), dim3(kWave), 0, stream, parts.o, parts.ml,
-                       splits, query_heads, head_dim, out, lse);
+    hipLaunchKernelGGL((merge_splits_kernel<64, uint32_t>), grid, dim3(kWave), 0, stream, parts.o, parts.ml, splits,
+                       query_heads, head_dim, out, lse);
   return hip_status(hipGetLastError(), "merge_splits launch");
 }
 
