@@ -54,8 +54,9 @@ __device__ __forceinline__ i32x2 lds_read_tr4(const uint8_t* lds, int offset) {
 // LDS copies, dynamic register indexing or messages), so the asm owns it.
 // NT: non-temporal hint, for the code arrays, read once per decode (streaming
 // reads measured ~8% faster with it).  Scale rows keep the default policy:
-// other workgroups of the split read the rest of each 128-byte scale line
-// from the same L2.
+// with 4 kv heads per workgroup the split's other workgroup reads the rest of
+// each 128-byte scale line from the same L2, and with 8 the hint on the scale
+// copies measured slower as well (+0.7 us on a 128K-token INT4 decode).
 template <bool NT>
 __device__ __forceinline__ void dma16(const uint8_t* sbase, uint32_t voff, uint32_t lds_dst) {
   if constexpr (NT)
