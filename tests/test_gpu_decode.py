@@ -371,3 +371,39 @@ def test_merge_of_more_than_256_splits(cuda_device):
     query, batch = to_device(cuda_device, q, pk, pv, sk, sv, empty, 4, 32)
     out, lse = HipAttentionBackend("auto").run(query, batch, 0.2)
     assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_staged_eight_kv_heads_stage_boundaries(cuda_device, bits):
+    # 8 kv heads per workgroup with three groups (24 kv heads) and 256-token
+    # blocks (four 64-token stages each): valid counts at and around stage
+    # boundaries, and empty blocks at split starts
+    rng = np.random.default_rng(500 + bits)
+    nb, bt, kvh, qh = 100, 256, 24, 48
+    q, pk, pv, sk, sv, _ = make_batch(31, qh, kvh, 128, nb, bt, bits, 32)
+    edges = np.array([0, 1, 63, 64, 65, 127, 128, 129, 191, 192, 255, 256], np.int32)
+    valid = edges[rng.integers(0, len(edges), nb)].astype(np.int32)
+    valid[::5] = 0
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, qdtype=torch.float16)
+    qq = torch.from_numpy(q).to(torch.float16).float().numpy()
+    ref_out, ref_lse = O.attention(qq, pk, pv, sk, sv, valid, bits, 32, 0.1, threads=16)
+    out, lse = HipAttentionBackend("staged").run(query, batch, 0.1)
+    check(out, lse, ref_out, ref_lse)
+
+
+def test_staged_eight_kv_heads_gqa8_reversed_table(cuda_device):
+    # just past the 2048 (kv head, block) pairs that select 8 kv heads per
+    # workgroup, GQA 8 (two query quads per wave), blocks attended in reverse
+    # order through a table
+    rng = np.random.default_rng(808)
+    nb = 260
+    q, pk, pv, sk, sv, _ = make_batch(44, 64, 8, 128, nb, 128, 4, 32)
+    valid = rng.integers(1, 129, nb).astype(np.int32)
+    ids = list(range(nb - 1, -1, -1))
+    ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.1, block_table=np.array(ids, np.int32), threads=16)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, 4, 32)
+    out, lse = HipAttentionBackend("staged").run(query, batch, 0.1, block_table=ids)
+    check(out, lse, ref_out, ref_lse)
+    out, lse = HipAttentionBackend("staged").run(query, batch, 0.1)
+    ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.1, threads=16)
+    check(out, lse, ref_out, ref_lse)
