@@ -201,7 +201,7 @@ def codec(torch, dev, args) -> int:
 
         # fp16 K and V read, whole records written
         nbytes = 2 * tokens * KV_HEADS * HEAD_DIM * 2 + nb * spec.record_bytes
-        name = "encode_payload_kernel + encode_header_kernel"
+        name = "encode_fused_kernel"
     for i in range(args.warmup):
         launch(i)
     torch.cuda.synchronize()

@@ -8,7 +8,8 @@
 // * quantize: bit-exact twin of quantize_tensor (src/kvssd/quant.py:49-65);
 // * encode: KVCacheStore.create's block loop for one layer (zero-padded last
 //   block, src/kvssd/store.py:46-63) -- quantise keys and values and write
-//   whole records with their CRC-32 (encode_record, format.py:104-131).
+//   whole records with their CRC-32 (encode_record, format.py:104-131); one
+//   fused kernel for the common layouts, else a payload and a header pass.
 //
 // CRC-32 machinery (zlib's CRC, chunked and general forms): crc32.hpp.
 #include "crc32.hpp"
@@ -197,8 +198,14 @@ __device__ __forceinline__ void quantize_group(const T* src, int group_size, int
 // in one 4-byte aligned store of 4 (INT4) or 2 (INT2) words.
 constexpr int kRegGroup = 32;
 
+template <int BITS>
+struct GroupWords {
+  uint32_t w[kRegGroup * BITS / 32];  // packed codes, low bits first
+  uint16_t scale;                     // fp16 bits
+};
+
 template <typename T, int BITS>
-__device__ __forceinline__ void quantize_group_reg(const T* src, uint8_t* packed, uint16_t* scale) {
+__device__ __forceinline__ GroupWords<BITS> quantize_group_words(const T* src) {
   float x[kRegGroup];
   if (src) {
     T v[kRegGroup];
@@ -214,17 +221,23 @@ __device__ __forceinline__ void quantize_group_reg(const T* src, uint8_t* packed
   for (int i = 0; i < kRegGroup; ++i) amax = fmaxf(amax, fabsf(x[i]));
   constexpr int mid = 1 << (BITS - 1);
   const float s32 = fmaxf(amax, 1e-8f) / static_cast<float>(mid - 1);
-  constexpr int words = kRegGroup * BITS / 32;
-  uint32_t w[words];
+  GroupWords<BITS> g;
 #pragma unroll
-  for (int k = 0; k < words; ++k) w[k] = 0;
+  for (int k = 0; k < kRegGroup * BITS / 32; ++k) g.w[k] = 0;
 #pragma unroll
   for (int i = 0; i < kRegGroup; ++i) {
     const float c = fminf(fmaxf(rintf(x[i] / s32), static_cast<float>(-mid)), static_cast<float>(mid - 1));
-    w[(i * BITS) >> 5] |= static_cast<uint32_t>(static_cast<int>(c) + mid) << ((i * BITS) & 31);
+    g.w[(i * BITS) >> 5] |= static_cast<uint32_t>(static_cast<int>(c) + mid) << ((i * BITS) & 31);
   }
-  __builtin_memcpy(__builtin_assume_aligned(packed, 4), w, sizeof(w));
-  *scale = __builtin_bit_cast(uint16_t, static_cast<_Float16>(s32));
+  g.scale = __builtin_bit_cast(uint16_t, static_cast<_Float16>(s32));
+  return g;
+}
+
+template <typename T, int BITS>
+__device__ __forceinline__ void quantize_group_reg(const T* src, uint8_t* packed, uint16_t* scale) {
+  const GroupWords<BITS> g = quantize_group_words<T, BITS>(src);
+  __builtin_memcpy(__builtin_assume_aligned(packed, 4), g.w, sizeof(g.w));
+  *scale = g.scale;
 }
 
 // BITS == 0: any group size (quantize_group); BITS == 2 / 4: group_size 32
@@ -342,6 +355,116 @@ __global__ __launch_bounds__(kCrcThreads) void encode_header_kernel(EncodeParams
   if (threadIdx.x == 0) p.crcs[r] = crc;
 }
 
+// One kernel for the common layout (group size 32 in registers, the scale
+// region [Ks | Vs] and the code region [Kc | Vc] each a whole number of
+// 16 KiB rows of the chunked CRC form, so no virtual zeros): one workgroup of
+// 1024 threads per record.  Thread t owns code chunks t, t + 1024, ... (rows
+// rs .. rows - 1 of the chunked form): it quantises their groups (one INT4
+// group or two INT2 groups per 16-byte chunk), stores each chunk, keeps it
+// in registers and puts the scales into an LDS copy of the scale region.
+// After a barrier it stores and reads back its scale chunks (rows 0 .. rs - 1)
+// from LDS and folds the record's CRC-32 from registers as the gather does, so
+// the payload is never read back; the header and padding follow.
+struct FusedPlan {
+  int rows_s, rows_c;  // rows of scale / code chunks
+};
+
+constexpr int kMaxScaleRows = 4;  // scale region <= 64 KiB of LDS
+constexpr int kMaxCodeRows = 8;   // code chunks kept in registers for the CRC
+
+template <typename T, int BITS>
+__global__ __launch_bounds__(kCrcThreads) void encode_fused_kernel(EncodeParams p, ChunkPlan c, FusedPlan f) {
+  __shared__ ChunkLds lds;
+  __shared__ __attribute__((aligned(16))) uint16_t scales[kMaxScaleRows * kStrideBytes / 2];
+  constexpr int kGroupsPerChunk = 4 / BITS;  // 32-value groups in 16 bytes of codes
+  const Layout& L = p.lay;
+  const int r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int G = L.head_dim / kRegGroup;
+  const int64_t per_array = static_cast<int64_t>(L.block_tokens) * L.kv_heads * G;  // groups per array
+  uint8_t* rec = p.records + static_cast<int64_t>(r) * L.record_bytes();
+  uint8_t* pay = rec + kHeaderBytes;
+  const int64_t code0 = 2 * L.scale_bytes();
+  load_chunk_tables(lds);
+  u32x4 code[kMaxCodeRows];
+#pragma unroll
+  for (int k = 0; k < kMaxCodeRows; ++k) {
+    code[k] = u32x4{0u, 0u, 0u, 0u};
+    if (k < f.rows_c) {
+      const int64_t chunk = static_cast<int64_t>(k) * kCrcThreads + tid;  // within the code region
+      uint32_t w[4];
+#pragma unroll
+      for (int i = 0; i < kGroupsPerChunk; ++i) {
+        const int64_t q = chunk * kGroupsPerChunk + i;  // over [K groups | V groups]
+        const bool is_v = q >= per_array;
+        const int64_t qa = is_v ? q - per_array : q;
+        const int64_t row = qa / G;  // token * kv_heads + head within the block
+        const int gi = static_cast<int>(qa % G);
+        const int64_t token = static_cast<int64_t>(r) * L.block_tokens + row / L.kv_heads;
+        const T* base = static_cast<const T*>(is_v ? p.values : p.keys);
+        const T* src =
+            token < p.tokens ? base + (token * L.kv_heads + row % L.kv_heads) * L.head_dim + gi * kRegGroup : nullptr;
+        const GroupWords<BITS> g = quantize_group_words<T, BITS>(src);
+        constexpr int kWords = kRegGroup * BITS / 32;
+#pragma unroll
+        for (int k2 = 0; k2 < kWords; ++k2) w[i * kWords + k2] = g.w[k2];
+        scales[q] = g.scale;
+      }
+      code[k] = u32x4{w[0], w[1], w[2], w[3]};
+      __builtin_memcpy(__builtin_assume_aligned(pay + code0 + chunk * kChunkBytes, 4), &code[k], kChunkBytes);
+    }
+  }
+  __syncthreads();  // every scale is in LDS (and the CRC tables)
+  uint32_t h = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxScaleRows; ++j) {
+    if (j < f.rows_s) {
+      const int64_t chunk = static_cast<int64_t>(j) * kCrcThreads + tid;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(scales) + chunk * kChunkBytes);
+      __builtin_memcpy(__builtin_assume_aligned(pay + chunk * kChunkBytes, 4), &v, kChunkBytes);
+      h = mul_stride(lds, h) ^ crc16_raw(lds, v);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kMaxCodeRows; ++k)
+    if (k < f.rows_c) h = mul_stride(lds, h) ^ crc16_raw(lds, code[k]);
+  const uint32_t crc = fold_chunks(lds, c, h);
+  const int64_t start = static_cast<int64_t>(r) * L.block_tokens;
+  const int64_t valid = p.tokens - start < L.block_tokens ? p.tokens - start : L.block_tokens;
+  if (tid < kHeaderBytes / 4) {
+    uint32_t v = 0;
+    switch (tid) {
+      case 0: v = kMagic0; break;
+      case 1: v = kMagic1; break;
+      case 2: v = 1u; break;
+      case 3: v = static_cast<uint32_t>(p.layer); break;
+      case 4: v = static_cast<uint32_t>(p.first_block + r); break;
+      case 5: v = static_cast<uint32_t>(valid); break;
+      case 6: v = static_cast<uint32_t>(L.bits); break;
+      case 7: v = static_cast<uint32_t>(L.block_tokens); break;
+      case 8: v = static_cast<uint32_t>(L.kv_heads); break;
+      case 9: v = static_cast<uint32_t>(L.head_dim); break;
+      case 10: v = static_cast<uint32_t>(L.group_size); break;
+      case 11: v = p.plan.len; break;
+      default: v = crc; break;
+    }
+    reinterpret_cast<uint32_t*>(rec)[tid] = v;
+  }
+  for (int64_t i = kHeaderBytes + L.payload_bytes() + tid; i < L.record_bytes(); i += kCrcThreads) rec[i] = 0;
+  if (tid == 0) p.crcs[r] = crc;
+}
+
+// the fused form applies (register groups checked separately): scale and code
+// regions whole rows of the chunked CRC form, scales within the LDS copy
+bool fused_layout(const Layout& L, FusedPlan* f) {
+  const int64_t sr = 2 * L.scale_bytes(), cr = 2 * L.packed_bytes();
+  if (L.group_size != kRegGroup || sr % kStrideBytes || cr % kStrideBytes) return false;
+  f->rows_s = static_cast<int>(sr / kStrideBytes);
+  f->rows_c = static_cast<int>(cr / kStrideBytes);
+  return f->rows_s >= 1 && f->rows_s <= kMaxScaleRows && f->rows_c >= 1 && f->rows_c <= kMaxCodeRows &&
+         f->rows_s + f->rows_c <= kMaxRows;
+}
+
 // the chunked CRC / gather form applies: all four arrays 16-byte multiples and
 // the payload at most kMaxRows rows of chunks
 bool chunked_layout(const Layout& L) {
@@ -380,6 +503,15 @@ void launch_quantize_t(const void* x, int64_t groups, int group_size, int bits, 
   } else {
     hipLaunchKernelGGL((quantize_kernel<T, 0>), grid, dim3(256), 0, s, src, groups, group_size, bits, packed, scales);
   }
+}
+
+template <typename T>
+void launch_fused_t(const EncodeParams& p, const ChunkPlan& c, const FusedPlan& f, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(p.n));
+  if (p.lay.bits == 4)
+    hipLaunchKernelGGL((encode_fused_kernel<T, 4>), grid, dim3(kCrcThreads), 0, s, p, c, f);
+  else
+    hipLaunchKernelGGL((encode_fused_kernel<T, 2>), grid, dim3(kCrcThreads), 0, s, p, c, f);
 }
 
 template <typename T>
@@ -491,6 +623,18 @@ int launch_encode_records(const kvssd_record_layout* layout, int dtype, const vo
   p.plan = make_crc_plan(static_cast<uint32_t>(L.payload_bytes()));
   p.records = records;
   p.crcs = crcs;
+  const uint32_t len = p.plan.len;
+  const ChunkPlan c = make_chunk_plan(len);
+  FusedPlan f{};
+  // (fp64 input keeps the two-kernel form: its fused INT2 instance would spill)
+  if (fused_layout(L, &f) && register_groups(L.group_size, keys, records) &&
+      (reinterpret_cast<uintptr_t>(values) & 15u) == 0 &&
+      (dtype == KVSSD_DTYPE_F16 || dtype == KVSSD_DTYPE_BF16 || dtype == KVSSD_DTYPE_F32)) {
+    if (dtype == KVSSD_DTYPE_F16) launch_fused_t<_Float16>(p, c, f, stream);
+    else if (dtype == KVSSD_DTYPE_BF16) launch_fused_t<uint16_t>(p, c, f, stream);
+    else launch_fused_t<float>(p, c, f, stream);
+    return hip_status(hipGetLastError(), "encode_records launch");
+  }
   switch (dtype) {
     case KVSSD_DTYPE_F16:
       launch_encode_t<_Float16>(p, stream);
@@ -508,8 +652,6 @@ int launch_encode_records(const kvssd_record_layout* layout, int dtype, const vo
       return arg_error("quantization input must be floating point");
   }
   if (int rc = hip_status(hipGetLastError(), "encode_records launch")) return rc;
-  const uint32_t len = p.plan.len;
-  const ChunkPlan c = make_chunk_plan(len);
   if (len % kChunkBytes == 0 && c.rows <= kMaxRows) {
     hipLaunchKernelGGL(encode_header_kernel<true>, dim3(static_cast<unsigned>(p.n)), dim3(kCrcThreads), 0, stream, p, c);
   } else {
