@@ -16,7 +16,11 @@ since the GPU needs tens of milliseconds of work to reach its steady clocks
 and a short warmup reads ~8% slow); ``roofline.achieved`` is the same bytes over the
 dominant (split) kernel's average duration: a second pass launches the split
 kernel alone K times back to back between two HIP events on its stream.
-``cpu_baseline`` is the CPU oracle (a plain-C port of the reference's
+``step_us`` gives p10 / p50 / p90 of single steps (an event pair around each).
+``pipeline`` times the public Python path, ``KVSSDPipeline.decode`` on layers
+resident in HBM (selection, argument checks, allocation and the fp16 cast
+included), over a store of the workload's shape written to a temporary
+directory.  ``cpu_baseline`` is the CPU oracle (a plain-C port of the reference's
 dequantise-then-attend path) timed on this host's cores over a bounded sample
 of the same workload.
 
@@ -103,6 +107,73 @@ def make_cache(torch, dev, tokens, bits, qh, value_scale, outliers, seed=7):
     query = torch.randn(qh, HEAD_DIM, generator=gen, device=dev, dtype=torch.float16)
     valid = torch.full((tokens // BLOCK_TOKENS,), BLOCK_TOKENS, dtype=torch.int32, device=dev)
     return query, out, valid
+
+
+def step_percentiles(torch, stream, step, steps: int) -> dict:
+    """p10 / p50 / p90 of single decode steps: an event pair around each of K steps."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i, (a, b) in enumerate(evs):
+        a.record(stream)
+        step(i)
+        b.record(stream)
+    torch.cuda.synchronize()
+    us = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)
+
+    def pick(f: float) -> float:
+        return round(us[min(len(us) - 1, int(f * len(us)))], 2)
+
+    return {"p10": pick(0.1), "p50": pick(0.5), "p90": pick(0.9), "timing": "an event pair around each of K steps"}
+
+
+def pipeline_leg(torch, dev, tokens: int, bits: int, qh: int, sel, steps: int, warmup: int, layers: int = 4) -> dict:
+    """KVSSDPipeline.decode(query, layer, selector) on layers resident in HBM.
+
+    The public Python path, host work included (selection, argument checks,
+    output allocation, the fp16 cast): a KVCacheStore of ``layers`` layers of
+    the workload's shape is written to a temporary directory, every layer is
+    made resident, and the steps cycle through the layers (together larger
+    than the Infinity Cache) as a decode over a model's layers does."""
+    import tempfile
+
+    from kvssd import KVCacheStore, KVSSDPipeline
+    from kvssd.format import CacheSpec
+    from kvssd.selectors import AllBlocks, RecentSinkBlocks
+
+    gen = torch.Generator(device=dev).manual_seed(11)
+    spec = CacheSpec(layers, KV_HEADS, HEAD_DIM, BLOCK_TOKENS, bits, GROUP)
+    selector = AllBlocks() if sel is None else RecentSinkBlocks(*sel)
+    with tempfile.TemporaryDirectory(prefix="kvssd_bench_") as root:
+        shape = (layers, tokens, KV_HEADS, HEAD_DIM)
+        keys = torch.randn(shape, generator=gen, device=dev, dtype=torch.float16)
+        values = torch.randn(shape, generator=gen, device=dev, dtype=torch.float16)
+        store = KVCacheStore.create(root, keys, values, spec)
+        del keys, values
+        query = torch.randn(qh, HEAD_DIM, generator=gen, device=dev, dtype=torch.float16)
+        with store, KVSSDPipeline(store, device=dev, attention_backend="hip") as pipe:
+            pipe.load_resident()
+            for i in range(warmup):
+                pipe.decode(query, i % layers, selector)
+            stream = torch.cuda.current_stream(dev)
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            start.record(stream)
+            for i in range(steps):
+                out = pipe.decode(query, i % layers, selector)
+            end.record(stream)
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            kernel = pipe.attention_backend.last_kernel
+            ok = bool(torch.isfinite(out).all().item())
+    return {
+        "us_per_step": round(wall / steps * 1e6, 2),
+        "gpu_us_per_step": round(start.elapsed_time(end) * 1e3 / steps, 2),
+        "path": f"KVSSDPipeline.decode over {layers} HBM-resident layers in turn, "
+        f"{'AllBlocks' if sel is None else f'RecentSinkBlocks{tuple(sel)}'}, hip backend, fp16 output",
+        "kernel": kernel,
+        "finite": ok,
+    }
 
 
 def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 20.0):
@@ -455,6 +526,9 @@ def main() -> int:
     ap.add_argument("--copies", type=int, default=0, help="distinct KV copies rotated across steps (0 = auto)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument(
+        "--no-pipeline", action="store_true", help="skip the KVSSDPipeline.decode leg (decode workloads)"
+    )
+    ap.add_argument(
         "--copy-calibration",
         type=int,
         default=0,
@@ -571,6 +645,8 @@ def main() -> int:
     torch.cuda.synchronize()
     kern_avg = k_start.elapsed_time(k_end) / args.steps
 
+    pct = step_percentiles(torch, stream, step, args.steps)
+
     gbps = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (kern_avg * 1e-3) / 1e9
     # quick numerical sanity on the last step's output against the portable path
@@ -613,6 +689,7 @@ def main() -> int:
             "alg_bytes_per_step": nbytes,
         },
         "kernel_us": {"avg": round(kern_avg * 1e3, 2), "timing": "K split launches back to back between two events"},
+        "step_us": pct,
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
@@ -625,6 +702,8 @@ def main() -> int:
         "host_wall_ms_per_step": round(wall / args.steps * 1e3, 4),
         "finite": ok,
     }
+    if not args.no_pipeline:
+        line["pipeline"] = pipeline_leg(torch, dev, tokens, bits, qh, sel, args.steps, args.warmup)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, query, {k: batches[0].__dict__[n] for k, n in (("pk", "packed_k"), ("pv", "packed_v"), ("sk", "scales_k"), ("sv", "scales_v"))}, valid, bits, table)
     print(json.dumps(line), flush=True)

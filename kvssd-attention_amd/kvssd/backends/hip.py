@@ -44,6 +44,7 @@ class HipAttentionBackend:
             raise ValueError(f"unknown hip kernel '{kernel}'; choose one of: {', '.join(names)}")
         self.kernel = names[kernel]
         self.last_kernel: str | None = None
+        self._plans: dict[tuple[int, ...], tuple[int, int]] = {}
 
     # ------------------------------------------------------------ probe ---
     def probe(self, device: torch.device) -> BackendAvailability:
@@ -127,14 +128,11 @@ class HipAttentionBackend:
         pk, pv = batch.packed_k.contiguous(), batch.packed_v.contiguous()
         sk, sv = batch.scales_k.contiguous(), batch.scales_v.contiguous()
         valid = batch.valid_tokens.contiguous()
-        need = ctypes.c_size_t(0)
-        _native.check(lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(need)), "workspace")
-        kern = ctypes.c_int(0)
-        _native.check(lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(kern)), "decode_kernel")
+        need, kern = self._plan(lib, desc)
         with torch.cuda.device(query.device):
             out = torch.empty((query.shape[0], query.shape[1]), dtype=torch.float32, device=query.device)
             lse = torch.empty((query.shape[0],), dtype=torch.float32, device=query.device)
-            work = torch.empty((max(int(need.value), 1),), dtype=torch.uint8, device=query.device)
+            work = torch.empty((max(need, 1),), dtype=torch.uint8, device=query.device)
             stream = torch.cuda.current_stream(query.device)
             rc = lib.kvssd_hip_fused_decode(
                 ctypes.byref(desc),
@@ -152,7 +150,7 @@ class HipAttentionBackend:
                 _native.stream_handle(stream),
             )
         _native.check(rc, "kvssd_hip_fused_decode")
-        name = _native.KERNEL_NAMES[kern.value]
+        name = _native.KERNEL_NAMES[kern]
         # the library's AUTO demotion for buffers the faster kernels cannot load
         if name in ("pairs", "staged") and not self._staged_aligned(pk, pv, sk, sv):
             name = "mfma"
@@ -160,6 +158,24 @@ class HipAttentionBackend:
             name = "general"
         self.last_kernel = name
         return out, lse
+
+    def _plan(self, lib, desc: _native.DecodeDesc) -> tuple[int, int]:
+        """(workspace bytes, kernel id) of a decode shape, asked of the library once per shape."""
+        key = (
+            desc.query_heads, desc.kv_heads, desc.head_dim, desc.num_blocks, desc.block_tokens,
+            desc.bits, desc.group_size, desc.query_dtype, desc.num_selected,
+        )
+        plan = self._plans.get(key)
+        if plan is None:
+            need = ctypes.c_size_t(0)
+            _native.check(lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(need)), "workspace")
+            kern = ctypes.c_int(0)
+            _native.check(lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(kern)), "decode_kernel")
+            plan = (int(need.value), int(kern.value))
+            if len(self._plans) >= 64:
+                self._plans.clear()
+            self._plans[key] = plan
+        return plan
 
     @staticmethod
     def _staged_aligned(pk, pv, sk, sv) -> bool:

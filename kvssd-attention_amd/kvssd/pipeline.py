@@ -25,7 +25,7 @@ from __future__ import annotations
 
 import math
 from collections.abc import Sequence
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import torch
 
@@ -42,6 +42,12 @@ from .store import KVCacheStore
 class _Resident:
     batch: PackedBatch
     row_of: dict[int, int]
+    ids: list[int]  # block id of each row, in row order
+    # device block tables of recent selections (selection -> int32 rows)
+    tables: dict[tuple[int, ...], torch.Tensor] = field(default_factory=dict)
+
+
+_TABLE_CACHE = 8  # selections whose device block tables a resident layer keeps
 
 
 class KVSSDPipeline:
@@ -136,20 +142,34 @@ class KVSSDPipeline:
             raise_for_status(status, layer, host.block_ids)
             del raw
             batch = PackedBatch(kp, vp, ks, vs, valid, spec.bits, spec.group_size)
-            self._resident[layer] = _Resident(batch, dict(host.row_of))
+            self._resident[layer] = _Resident(batch, dict(host.row_of), list(host.block_ids))
 
     def release_resident(self, layers: Sequence[int] | None = None) -> None:
         for layer in list(self._resident) if layers is None else layers:
             self._resident.pop(layer, None)
 
+    def _table(self, res: _Resident, selected: list[int]) -> torch.Tensor | None:
+        """Device block table for ``selected``; None when it is every row in order."""
+        if selected == res.ids:
+            return None
+        key = tuple(selected)
+        table = res.tables.get(key)
+        if table is None:
+            rows = [res.row_of[b] for b in selected]
+            table = torch.tensor(rows, dtype=torch.int32).to(self.device)
+            if len(res.tables) >= _TABLE_CACHE:
+                res.tables.pop(next(iter(res.tables)))
+            res.tables[key] = table
+        return table
+
     def _decode_resident(self, query: torch.Tensor, layer: int, selected: list[int]) -> torch.Tensor:
         res = self._resident[layer]
-        rows = [res.row_of[b] for b in selected]
         scale = 1.0 / math.sqrt(query.shape[-1])
         run = self.attention_backend.run
         if getattr(self.attention_backend, "name", None) == "hip":
-            out, _ = run(query, res.batch, scale, block_table=rows)
+            out, _ = run(query, res.batch, scale, block_table=self._table(res, selected))
         else:
+            rows = [res.row_of[b] for b in selected]
             idx = torch.tensor(rows, dtype=torch.long, device=self.device)
             b = res.batch
             sub = PackedBatch(

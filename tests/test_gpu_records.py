@@ -107,7 +107,7 @@ SPECS = [
 
 
 @pytest.mark.parametrize("spec", SPECS, ids=lambda s: f"b{s.bits}-kvh{s.kv_heads}-d{s.head_dim}-bt{s.block_tokens}")
-@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_encode_records_bit_exact(cuda_device, spec, dtype):
     gen = torch.Generator().manual_seed(11)
     tokens = 3 * spec.block_tokens - 1  # partial last block
