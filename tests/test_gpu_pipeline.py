@@ -64,6 +64,36 @@ def test_resident_pipeline_matches_streamed(cuda_device, tmp_path: Path):
     np.testing.assert_allclose(full.float().cpu().numpy(), ref_full, atol=ATOL, rtol=RTOL)
 
 
+class _Ids:
+    """A selector returning fixed block ids (any order, repeats allowed)."""
+
+    def __init__(self, ids):
+        self.ids = list(ids)
+
+    def select(self, available):
+        return list(self.ids)
+
+
+def test_resident_decode_over_many_selections(cuda_device, tmp_path: Path):
+    """More distinct selections than the resident layer keeps device tables for,
+    visited twice (tables built, evicted and rebuilt), each against the oracle;
+    the whole layer in order takes the no-table form, a permutation of it does not."""
+    store, (pk, pv, sk, sv, valid) = build_store(tmp_path, 2500, 4)  # 20 blocks
+    query = torch.randn(32, 128, generator=torch.Generator().manual_seed(5), dtype=torch.float16)
+    scale = 1 / math.sqrt(128)
+    q = query.float().numpy()
+    selectors = [RecentSinkBlocks(1, r) for r in range(1, 12)] + [AllBlocks(), _Ids(range(19, -1, -1))]
+    with KVSSDPipeline(store, device=cuda_device, attention_backend="hip") as pipe:
+        pipe.load_resident([0])
+        for _ in range(2):
+            for sel in selectors:
+                out = pipe.decode(query, 0, sel)
+                ids = np.array(sel.select(list(range(20))), np.int32)
+                ref, _ = O.attention(q, pk, pv, sk, sv, valid, 4, 32, scale, block_table=ids)
+                np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+        assert len(pipe._resident[0].tables) <= 8
+
+
 def test_require_cuda_kernel_runs_hip(cuda_device, tmp_path: Path):
     store, _ = build_store(tmp_path, 300, 4)
     with KVSSDPipeline(store, device=cuda_device, require_cuda_kernel=True) as pipe:
