@@ -56,6 +56,8 @@ WORKLOAD_LABELS = {
     "int2_gqa_128k": "INT2 GQA 128K tokens",
     "int4_gqa_4k": "INT4 GQA 4K tokens",
     "int4_gqa8_256k_sparse": "INT4 GQA 8, 256K tokens, RecentSinkBlocks(1, 32)",
+    "int4_gqa_256k": "INT4 GQA 256K tokens",
+    "int4_gqa_1m": "INT4 GQA 1M tokens (HBM-resident)",
 }
 HBM_PEAK_GBPS = 8000.0
 
@@ -65,6 +67,9 @@ WORKLOADS = {
     "int4_gqa_128k": (131072, 4, 32, 0.5, 0.0, None),
     "int2_gqa_128k": (131072, 2, 32, 1.0, 0.05, None),
     "int4_gqa8_256k_sparse": (262144, 4, 64, 1.0, 0.0, (1, 32)),
+    # longer contexts of the same shape, resident in HBM (context-length scaling)
+    "int4_gqa_256k": (262144, 4, 32, 0.5, 0.0, None),
+    "int4_gqa_1m": (1048576, 4, 32, 0.5, 0.0, None),
 }
 # name -> (tokens, bits, query_heads, stage_blocks): records in page-locked host memory
 HOST_STAGED = {
@@ -703,7 +708,9 @@ def main() -> int:
         "finite": ok,
     }
     if not args.no_pipeline:
-        line["pipeline"] = pipeline_leg(torch, dev, tokens, bits, qh, sel, args.steps, args.warmup)
+        # enough layers to pass the Infinity Cache, at most 4 (1 at 1M tokens)
+        layers = max(1, min(4, math.ceil(1.2e9 / alg_bytes(nb, bits))))
+        line["pipeline"] = pipeline_leg(torch, dev, tokens, bits, qh, sel, args.steps, args.warmup, layers)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch, query, {k: batches[0].__dict__[n] for k, n in (("pk", "packed_k"), ("pv", "packed_v"), ("sk", "scales_k"), ("sv", "scales_v"))}, valid, bits, table)
     print(json.dumps(line), flush=True)
