@@ -546,7 +546,7 @@ def main() -> int:
         args.warmup = 2000 if args.workload in WORKLOADS and not args.copy_calibration else 20
     if args.gpus != 1:
         print(
-            "bench.py measures one GPU only: this build has no multi-GPU path "
+            "bench.py measures one GPU only: the library has no multi-GPU path "
             "(the decode would shard by kv head or by token range across GPUs)",
             file=sys.stderr,
         )

@@ -11,7 +11,7 @@ from .backends import AttentionBackend, PackedBatch, resolve_attention_backend
 from .format import PackedKVBlock
 from .quant import dequantize_tensor
 
-# The fused native kernel of this build.  ``require_cuda_kernel=True`` in the
+# The fused native kernel here is the HIP one.  ``require_cuda_kernel=True`` in the
 # reference means "the fused native kernel must run"; on ROCm that kernel is
 # the ``hip`` backend, so the flag resolves to it.
 NATIVE_BACKEND = "hip"

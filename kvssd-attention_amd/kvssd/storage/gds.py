@@ -1,8 +1,8 @@
 """GPUDirect Storage placeholder.
 
 The reference's cuFile tier (src/kvssd/storage/gds.py:13-97,
-csrc/gds_bindings.cpp) needs NVIDIA's libcufile and has no ROCm counterpart in
-this build.  The name stays registered so ``available_storage_backends`` keeps
+csrc/gds_bindings.cpp) needs NVIDIA's libcufile and has no ROCm counterpart
+here.  The name stays registered so ``available_storage_backends`` keeps
 the reference's shape and an explicit ``"gds"`` request fails closed with the
 reason instead of silently changing the data path.
 """

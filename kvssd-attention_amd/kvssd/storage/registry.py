@@ -1,6 +1,6 @@
 """Storage backend registry (reference: src/kvssd/storage/registry.py:12-66).
 
-Automatic selection tries ``gds`` (never available in this build), then
+Automatic selection tries ``gds`` (never available on ROCm), then
 ``direct``, then ``buffered``; an explicit name fails closed with the backend's
 reason.
 """

@@ -2,7 +2,7 @@
  * CPU oracle for the fused INT2/INT4 dequant + decode-attention path.
  *
  * TEST INFRASTRUCTURE ONLY.  This file is a plain-C restatement of the
- * reference algorithm, used as the checker by tests/, by
+ * reference algorithm, used to check results by tests/, by
  * __graft_entry__.smoke() and by bench.py's cpu_baseline leg.  Nothing in the
  * kvssd package links, loads or calls it; the product path never routes
  * through it.

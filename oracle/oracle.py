@@ -1,7 +1,7 @@
 """CPU oracle for the fused INT2/INT4 decode-attention path.
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
-``bench.py``'s cpu_baseline leg import this module, and only as the checker.
+``bench.py``'s cpu_baseline leg import this module, and only to check results.
 The ``kvssd`` package never imports it.
 
 It restates the reference algorithm from its source (citations per function):
