@@ -21,6 +21,9 @@ def test_more_than_one_gpu_exits_with_a_message():
 def test_help_names_the_workloads_and_the_warmup_default():
     proc = run_bench("--help")
     assert proc.returncode == 0
-    for name in ("int4_gqa_128k", "int2_gqa_128k", "int4_gqa_4k", "int4_gqa8_256k_sparse", "int4_gqa_1m_host_staged"):
+    for name in (
+        "int4_gqa_128k", "int2_gqa_128k", "int4_gqa_4k", "int4_gqa8_256k_sparse", "int4_gqa_256k", "int4_gqa_1m",
+        "int4_gqa_1m_host_staged",
+    ):
         assert name in proc.stdout
     assert "2000" in proc.stdout
