@@ -527,7 +527,7 @@ def main() -> int:
         "needs to reach its steady clocks; 20 otherwise)",
     )
     ap.add_argument("--workload", default="int4_gqa_128k", choices=sorted(WORKLOADS) + sorted(HOST_STAGED) + sorted(CODEC))
-    ap.add_argument("--kernel", default="auto", choices=["auto", "general", "mfma", "staged", "pairs"])
+    ap.add_argument("--kernel", default="auto", choices=["auto", "general", "mfma", "staged"])
     ap.add_argument("--copies", type=int, default=0, help="distinct KV copies rotated across steps (0 = auto)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument(
@@ -676,7 +676,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if kernel_name in ("mfma", "staged", "pairs") else "f32",
+        "dtype": "f16" if kernel_name in ("mfma", "staged") else "f32",
         "data": "synthetic",
         "config": {
             "workload": args.workload,

@@ -45,11 +45,8 @@ enum kvssd_kernel {
   KVSSD_KERNEL_AUTO = 0,    /* fastest kernel that supports the shape */
   KVSSD_KERNEL_GENERAL = 1, /* any shape the reference accepts */
   KVSSD_KERNEL_MFMA = 2,    /* matrix-core kernel: head_dim 128, group_size 32 */
-  KVSSD_KERNEL_STAGED = 3,  /* LDS-staged matrix-core kernel: as MFMA, plus
+  KVSSD_KERNEL_STAGED = 3   /* LDS-staged matrix-core kernel: as MFMA, plus
                                kv_heads % 4 == 0 and 16-byte aligned arrays */
-  KVSSD_KERNEL_PAIRS = 4    /* pair-owned LDS-staged matrix-core kernel: as
-                               STAGED, INT4 only, <= 4 query heads per kv head;
-                               used only when named (AUTO picks STAGED) */
 };
 
 /* Shape of one decode call.  The packed arrays follow the reference's
@@ -57,9 +54,13 @@ enum kvssd_kernel {
  *   packed_k, packed_v  uint8   [num_blocks, block_tokens, kv_heads, head_dim*bits/8]
  *   scales_k, scales_v  float16 [num_blocks, block_tokens, kv_heads, head_dim/group_size]
  *   valid_tokens        int32   [num_blocks]
- * all C-contiguous.  When block_table is not NULL it lists num_selected block
- * ids (int32, each in [0, num_blocks)) and the call attends over those blocks
- * in table order; with NULL it attends over blocks 0..num_blocks-1. */
+ * all C-contiguous.  When block_table is not NULL it lists num_selected >= 1
+ * block ids (int32, each in [0, num_blocks)) and the call attends over those
+ * blocks in table order; with NULL, num_selected must be 0 and the call attends
+ * over blocks 0..num_blocks-1.  The entry points without a table argument
+ * (kvssd_hip_decode_workspace_bytes, kvssd_hip_decode_kernel,
+ * kvssd_hip_decode_merge) plan for num_selected blocks when it is > 0, else for
+ * num_blocks, so they agree with the call that passes the table. */
 typedef struct kvssd_decode_desc {
   int32_t query_heads;
   int32_t kv_heads;
@@ -69,7 +70,7 @@ typedef struct kvssd_decode_desc {
   int32_t bits;
   int32_t group_size;
   int32_t query_dtype;  /* enum kvssd_dtype */
-  int32_t num_selected; /* entries in block_table; ignored when it is NULL */
+  int32_t num_selected; /* entries in block_table; 0 when there is none */
   int32_t kernel;       /* enum kvssd_kernel */
   double sm_scale;
 } kvssd_decode_desc;
@@ -95,8 +96,10 @@ int kvssd_hip_decode_kernel(const kvssd_decode_desc* desc, int* kernel);
  * scaled scores).  Replaces kvssd._C.fused_decode (csrc/bindings.cpp:16-41,
  * csrc/fused_decode.cu:92-143) with the semantics of
  * ReferenceAttentionBackend.run (src/kvssd/backends/reference.py:22-50):
- * valid_tokens[b] is clamped to [0, block_tokens]; with no valid token at all
- * out is 0 and lse is -inf.  `query` holds query_heads*head_dim elements of
+ * block b contributes the rows keys[b, :valid_tokens[b]] would keep in Python
+ * (reference.py:38-40): min(v, block_tokens) rows for v >= 0 and
+ * max(block_tokens + v, 0) rows for v < 0.  With no valid token at all out is
+ * 0 and lse is -inf.  `query` holds query_heads*head_dim elements of
  * query_dtype. */
 int kvssd_hip_fused_decode(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k,
                            const uint8_t* packed_v, const uint16_t* scales_k, const uint16_t* scales_v,
@@ -122,19 +125,19 @@ int kvssd_hip_decode_merge(const kvssd_decode_desc* desc, const void* workspace,
 /* Running exact merge of normalised attention chunks, in place:
  *   L = logaddexp(acc_lse, lse); acc_out = acc_out e^(acc_lse-L) + out e^(lse-L)
  * over `rows` rows of `dim` fp32 values.  Replaces merge_attention_chunks
- * (src/kvssd/attention.py:287-298) in the pipeline's chunk loop
+ * (src/kvssd/attention.py:91-102) in the pipeline's chunk loop
  * (src/kvssd/pipeline.py:147-153).  A chunk with lse = -inf adds nothing. */
 int kvssd_hip_merge_chunks(int rows, int dim, float* acc_out, float* acc_lse, const float* out, const float* lse,
                            void* stream);
 
 /* Unsigned codes of `n_bytes` packed bytes (8/bits codes per byte, low bits
  * first), unpacked by the same in-register routine the fused kernels use.
- * Bit-exact twin of unpack_codes (src/kvssd/quant.py:66-72). */
+ * Bit-exact twin of unpack_codes (src/kvssd/quant.py:40-46). */
 int kvssd_hip_unpack_codes(const uint8_t* packed, int bits, int64_t n_bytes, uint8_t* codes, void* stream);
 
 /* fp32 (code - mid) * scale for `rows` rows of `head_dim` elements
  * (packed [rows, head_dim*bits/8], scales [rows, head_dim/group_size]).
- * Twin of dequantize_tensor (src/kvssd/quant.py:94-99); exact. */
+ * Twin of dequantize_tensor (src/kvssd/quant.py:68-73); exact. */
 int kvssd_hip_dequantize(const uint8_t* packed, const uint16_t* scales, int64_t rows, int head_dim, int bits,
                          int group_size, float* out, void* stream);
 

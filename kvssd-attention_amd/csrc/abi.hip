@@ -50,23 +50,19 @@ int validate(const kvssd_decode_desc* d, int* units) {
   if (d->query_heads % d->kv_heads) return arg_error("query heads must be divisible by KV heads");
   if (d->head_dim > 256) return arg_error("head_dim must be <= 256");
   if (d->query_dtype < KVSSD_DTYPE_F16 || d->query_dtype > KVSSD_DTYPE_F64) return arg_error("unsupported query dtype");
-  if (d->kernel < KVSSD_KERNEL_AUTO || d->kernel > KVSSD_KERNEL_PAIRS) return arg_error("unknown kernel selector");
+  if (d->kernel < KVSSD_KERNEL_AUTO || d->kernel > KVSSD_KERNEL_STAGED) return arg_error("unknown kernel selector");
+  if (d->num_selected < 0) return arg_error("num_selected must be >= 0");
   *units = d->num_blocks;
   return 0;
 }
 
-// Kernel for a shape (pointer alignment can still demote PAIRS / STAGED ->
-// MFMA -> GENERAL under AUTO, see kvssd_hip_decode_partials).
+// Kernel for a shape (pointer alignment can still demote STAGED -> MFMA ->
+// GENERAL under AUTO, see kvssd_hip_decode_partials).
 int choose_kernel(const kvssd_decode_desc& d, int* kernel) {
-  std::string why_mfma, why_staged, why_pairs;
+  std::string why_mfma, why_staged;
   const bool mfma = mfma_supported(d, &why_mfma);
   const bool staged = mfma && staged_supported(d, &why_staged);
-  const bool pairs = mfma && pairs_supported(d, &why_pairs);
-  if (d.kernel == KVSSD_KERNEL_PAIRS) {
-    if (!mfma) return arg_error("pair-owned matrix-core kernel does not support this shape: " + why_mfma);
-    if (!pairs) return arg_error("pair-owned matrix-core kernel does not support this shape: " + why_pairs);
-    *kernel = KVSSD_KERNEL_PAIRS;
-  } else if (d.kernel == KVSSD_KERNEL_STAGED) {
+  if (d.kernel == KVSSD_KERNEL_STAGED) {
     if (!mfma) return arg_error("staged matrix-core kernel does not support this shape: " + why_mfma);
     if (!staged) return arg_error("staged matrix-core kernel does not support this shape: " + why_staged);
     *kernel = KVSSD_KERNEL_STAGED;
@@ -76,32 +72,49 @@ int choose_kernel(const kvssd_decode_desc& d, int* kernel) {
   } else if (d.kernel == KVSSD_KERNEL_GENERAL) {
     *kernel = KVSSD_KERNEL_GENERAL;
   } else {
-    // (the pair-owned kernel is selected only explicitly: on the INT4 128K
-    // workloads it measures ~2 us slower than the staged one)
     *kernel = staged ? KVSSD_KERNEL_STAGED : mfma ? KVSSD_KERNEL_MFMA : KVSSD_KERNEL_GENERAL;
   }
   return 0;
 }
 
+// Blocks attended by a call.  num_selected is the block table's length: a
+// table needs num_selected >= 1, and num_selected must be 0 without one.  The
+// phases that take no table pointer (merge, workspace size) read the same
+// count from the descriptor, so every entry point plans the same splits.
 int units_of(const kvssd_decode_desc* d, const int32_t* table, int* units) {
   if (table != nullptr) {
     if (d->num_selected <= 0) return arg_error("at least one block is required");
     *units = d->num_selected;
+  } else if (d->num_selected != 0) {
+    return arg_error("num_selected must be 0 when block_table is NULL");
   }
   return 0;
 }
 
+// The attended-block count of a descriptor alone (no table pointer): the
+// phases without one plan from it.
+int units_of_desc(const kvssd_decode_desc* d, int* units) {
+  if (d->num_selected < 0) return arg_error("num_selected must be >= 0");
+  *units = d->num_selected > 0 ? d->num_selected : d->num_blocks;
+  return 0;
+}
+
 // Validation, unit count, kernel choice and split plan shared by the phases.
-int prepare(const kvssd_decode_desc* desc, const int32_t* table, void* workspace, size_t workspace_bytes, int* units,
-            int* kernel, int* splits) {
-  if (int rc = validate(desc, units)) return rc;
-  if (int rc = units_of(desc, table, units)) return rc;
+int plan_checked(const kvssd_decode_desc* desc, int units, const void* workspace, size_t workspace_bytes, int* kernel,
+                 int* splits) {
   if (int rc = choose_kernel(*desc, kernel)) return rc;
-  *splits = plan_splits(*desc, *units).splits;
+  *splits = plan_splits(*desc, units).splits;
   const size_t need = split_partial_bytes(*splits, desc->query_heads, desc->head_dim);
   if (workspace == nullptr || workspace_bytes < need)
     return arg_error("workspace too small: need " + std::to_string(need) + " bytes");
   return 0;
+}
+
+int prepare(const kvssd_decode_desc* desc, const int32_t* table, void* workspace, size_t workspace_bytes, int* units,
+            int* kernel, int* splits) {
+  if (int rc = validate(desc, units)) return rc;
+  if (int rc = units_of(desc, table, units)) return rc;
+  return plan_checked(desc, *units, workspace, workspace_bytes, kernel, splits);
 }
 
 }  // namespace
@@ -161,7 +174,7 @@ __attribute__((visibility("default"))) int kvssd_hip_decode_workspace_bytes(cons
   int units = 0;
   if (int rc = validate(desc, &units)) return rc;
   if (bytes == nullptr) return arg_error("bytes output pointer is NULL");
-  if (desc->num_selected > 0) units = desc->num_selected;
+  if (int rc = units_of_desc(desc, &units)) return rc;
   int kernel = 0;
   if (int rc = choose_kernel(*desc, &kernel)) return rc;
   *bytes = split_partial_bytes(plan_splits(*desc, units).splits, desc->query_heads, desc->head_dim);
@@ -189,12 +202,6 @@ __attribute__((visibility("default"))) int kvssd_hip_decode_partials(
   a.stream = static_cast<hipStream_t>(stream);
   SplitPartials parts = carve_partials(workspace, splits, desc->query_heads, desc->head_dim);
   const SplitPlan plan = plan_splits(*desc, units);
-  if (kernel == KVSSD_KERNEL_PAIRS) {
-    if (staged_aligned(a)) return launch_pairs(a, plan, parts);
-    if (desc->kernel == KVSSD_KERNEL_PAIRS)
-      return arg_error("pair-owned matrix-core kernel needs 16-byte aligned packed arrays and scales");
-    kernel = KVSSD_KERNEL_MFMA;
-  }
   if (kernel == KVSSD_KERNEL_STAGED) {
     if (staged_aligned(a)) return launch_staged(a, plan, parts);
     if (desc->kernel == KVSSD_KERNEL_STAGED)
@@ -213,10 +220,9 @@ __attribute__((visibility("default"))) int kvssd_hip_decode_merge(const kvssd_de
                                                                   const void* workspace, size_t workspace_bytes,
                                                                   float* out, float* lse, void* stream) {
   int units = 0, kernel = 0, splits = 0;
-  // the table pointer only matters for its NULL-ness: units come from the descriptor
-  const int32_t* marker = (desc && desc->num_selected > 0) ? reinterpret_cast<const int32_t*>(1) : nullptr;
-  if (int rc = prepare(desc, marker, const_cast<void*>(workspace), workspace_bytes, &units, &kernel, &splits))
-    return rc;
+  if (int rc = validate(desc, &units)) return rc;
+  if (int rc = units_of_desc(desc, &units)) return rc;
+  if (int rc = plan_checked(desc, units, workspace, workspace_bytes, &kernel, &splits)) return rc;
   if (!out || !lse) return arg_error("a required buffer pointer is NULL");
   SplitPartials parts = carve_partials(const_cast<void*>(workspace), splits, desc->query_heads, desc->head_dim);
   return launch_merge_splits(parts, splits, desc->query_heads, desc->head_dim, out, lse,

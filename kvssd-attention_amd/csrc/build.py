@@ -22,7 +22,7 @@ HERE = Path(__file__).resolve().parent
 PKG = HERE.parent / "kvssd"
 OUT = PKG / "libkvssd_hip.so"
 BUILD = HERE / "_build"
-SOURCES = ["abi.hip", "decode_general.hip", "decode_mfma.hip", "decode_staged.hip", "decode_pairs.hip", "merge.hip", "codec.hip", "records.hip", "vllm_codec.hip"]
+SOURCES = ["abi.hip", "decode_general.hip", "decode_mfma.hip", "decode_staged.hip", "merge.hip", "codec.hip", "records.hip", "vllm_codec.hip"]
 ARCH = "gfx950"
 
 COMMON = [

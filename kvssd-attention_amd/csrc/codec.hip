@@ -6,10 +6,10 @@
 //   code = F * (value - 1)   (value = 1 + code / F, F = 64 for INT4, 4 for INT2)
 // so any mistake in which code lands in which fp16 lane, or in the exponent
 // and mantissa placement, changes the output.  Twin of unpack_codes
-// (src/kvssd/quant.py:66-72).
+// (src/kvssd/quant.py:40-46).
 //
 // dequantize: (code - mid) * fp16 scale in fp32, the operation of
-// dequantize_tensor (src/kvssd/quant.py:94-99) and of
+// dequantize_tensor (src/kvssd/quant.py:68-73) and of
 // csrc/fused_decode.cu:53-56; exact in fp32.
 #include "decode.hpp"
 

@@ -76,8 +76,12 @@ __device__ __forceinline__ float load_query<double>(const void* q, int index) {
   return static_cast<float>(static_cast<const double*>(q)[index]);
 }
 
+// Rows of a block that take part in attention for its count v: the rows
+// Python's slice keys[block, :v] keeps (src/kvssd/backends/reference.py:38-40),
+// i.e. min(v, BT) for v >= 0 and max(BT + v, 0) for v < 0.
 __device__ __forceinline__ int clamp_valid(int v, int block_tokens) {
-  return v < 0 ? 0 : (v > block_tokens ? block_tokens : v);
+  const int n = v < 0 ? block_tokens + v : v;
+  return n < 0 ? 0 : (n > block_tokens ? block_tokens : n);
 }
 
 // Wave-wide reductions over the 64 lanes (result in every lane).

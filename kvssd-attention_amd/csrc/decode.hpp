@@ -44,11 +44,6 @@ bool staged_wide(const kvssd_decode_desc& d, int units);
 bool staged_aligned(const DecodeArgs& a);
 int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts);
 
-// ---- pair-owned LDS-staged matrix-core kernel: INT4, at most 4 query heads
-// per kv head, kv_heads % 4 == 0, 16-byte aligned arrays (staged_aligned)
-bool pairs_supported(const kvssd_decode_desc& d, std::string* why);
-int launch_pairs(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts);
-
 // ---- split-K phase 2: merge the partials of every split into (out, lse)
 int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, float* out, float* lse,
                         hipStream_t stream);

@@ -10,7 +10,7 @@
 // src/kvssd/backends/reference.py:46-49 returns it).
 //
 // merge_chunks: the pipeline's running merge of normalised chunk results,
-// src/kvssd/attention.py:287-298 (L = logaddexp(La, Lb),
+// src/kvssd/attention.py:91-102 (L = logaddexp(La, Lb),
 // O = Oa e^(La - L) + Ob e^(Lb - L)), fused into one launch.
 #include "decode.hpp"
 

@@ -1,5 +1,5 @@
-// Device helpers shared by the LDS-staged matrix-core decode kernels
-// (decode_staged.hip, decode_pairs.hip): operand types, the global -> LDS
+// Device helpers of the LDS-staged matrix-core decode kernel
+// (decode_staged.hip): operand types, the global -> LDS
 // copies, the in-register code -> fp16 unpack, the QK query operands and the
 // stage cursor.
 #pragma once

@@ -19,13 +19,12 @@ LIB_PATH = Path(__file__).resolve().parent / "libkvssd_hip.so"
 ABI_VERSION = 3
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3
-KERNEL_AUTO, KERNEL_GENERAL, KERNEL_MFMA, KERNEL_STAGED, KERNEL_PAIRS = 0, 1, 2, 3, 4
+KERNEL_AUTO, KERNEL_GENERAL, KERNEL_MFMA, KERNEL_STAGED = 0, 1, 2, 3
 KERNEL_NAMES = {
     KERNEL_AUTO: "auto",
     KERNEL_GENERAL: "general",
     KERNEL_MFMA: "mfma",
     KERNEL_STAGED: "staged",
-    KERNEL_PAIRS: "pairs",
 }
 
 QUERY_DTYPES = {

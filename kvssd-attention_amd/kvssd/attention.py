@@ -73,7 +73,7 @@ def native_backend_available() -> bool:
         return False
 
 
-# Name kept for API compatibility with the reference (src/kvssd/attention.py:259-264).
+# Name kept for API compatibility with the reference (src/kvssd/attention.py:63-68).
 cuda_extension_available = native_backend_available
 
 
@@ -123,7 +123,7 @@ def resolve_required(
     require_cuda_kernel: bool, attention_backend: str | AttentionBackend | None, device: torch.device
 ) -> AttentionBackend:
     """Backend resolution shared by packed_attention and the pipeline
-    (src/kvssd/attention.py:312-315, src/kvssd/pipeline.py:44-48)."""
+    (src/kvssd/attention.py:116-119, src/kvssd/pipeline.py:44-48)."""
     if require_cuda_kernel and not (
         attention_backend in _NATIVE_ALIASES
         or getattr(attention_backend, "name", None) == NATIVE_BACKEND

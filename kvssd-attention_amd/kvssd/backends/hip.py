@@ -92,7 +92,7 @@ class HipAttentionBackend:
         )
 
     def kernel_for(self, query: torch.Tensor, batch: PackedBatch, sm_scale: float = 1.0) -> str:
-        """Name of the kernel ``run`` would launch for this shape ("general", "mfma", "staged" or "pairs")."""
+        """Name of the kernel ``run`` would launch for this shape ("general", "mfma" or "staged")."""
         desc = self.describe(query, batch, sm_scale)
         out = ctypes.c_int(0)
         _native.check(_native.load().kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(out)), "decode_kernel")
@@ -152,7 +152,7 @@ class HipAttentionBackend:
         _native.check(rc, "kvssd_hip_fused_decode")
         name = _native.KERNEL_NAMES[kern]
         # the library's AUTO demotion for buffers the faster kernels cannot load
-        if name in ("pairs", "staged") and not self._staged_aligned(pk, pv, sk, sv):
+        if name == "staged" and not self._staged_aligned(pk, pv, sk, sv):
             name = "mfma"
         if name == "mfma" and not self._mfma_aligned(batch.bits, pk, pv, sk, sv):
             name = "general"

@@ -35,8 +35,9 @@ class ReferenceAttentionBackend:
 
         keys = dequant(batch.packed_k, batch.scales_k)
         values = dequant(batch.packed_v, batch.scales_v)
-        block_tokens = keys.shape[1]
-        counts = [max(0, min(block_tokens, int(v))) for v in batch.valid_tokens.tolist()]
+        # block i contributes the rows [i, :valid[i]] (Python slice rules: a
+        # negative count drops that many rows from the end of the block)
+        counts = [int(v) for v in batch.valid_tokens.tolist()]
         keys = torch.cat([keys[i, :n] for i, n in enumerate(counts)], dim=0)
         values = torch.cat([values[i, :n] for i, n in enumerate(counts)], dim=0)
         q_heads, kv_heads = query.shape[0], keys.shape[1]

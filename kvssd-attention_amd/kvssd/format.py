@@ -1,6 +1,6 @@
 """Fixed-size KV block record format, v1.
 
-The on-disk layout is the reference's (src/kvssd/format.py:13-276), byte for
+The on-disk layout is the reference's (src/kvssd/format.py:14-177), byte for
 byte, so stores written by either implementation open in the other:
 
 * a 52-byte little-endian header ``<8sIIIIIIIIIII``: magic ``KVSSD001``,

@@ -1,16 +1,16 @@
 """Symmetric groupwise INT2/INT4 codec.
 
-Semantics follow src/kvssd/quant.py:7-99 of the reference exactly, because the
+Semantics follow src/kvssd/quant.py:8-73 of the reference exactly, because the
 packed bytes and fp16 scales produced here are the input of the fused HIP
 kernel and must be bit-identical to what the reference writes:
 
 * ``scale32 = max(|x|).clamp_min(1e-8) / (2^(bits-1) - 1)`` per group of
-  ``group_size`` elements along the last dimension (quant.py:82);
+  ``group_size`` elements along the last dimension (quant.py:56);
 * ``code = clamp(round_half_even(x / scale32), -mid, mid - 1) + mid``
-  (quant.py:83-84), so codes are unsigned with midpoint ``mid = 2^(bits-1)``;
-* codes are packed low bits first within each byte (quant.py:54-63);
-* the stored scale is ``fp16(scale32)`` (quant.py:87) and dequantisation uses
-  that fp16 value: ``(code - mid) * float(scale)`` (quant.py:94-99).
+  (quant.py:57-58), so codes are unsigned with midpoint ``mid = 2^(bits-1)``;
+* codes are packed low bits first within each byte (quant.py:28-37);
+* the stored scale is ``fp16(scale32)`` (quant.py:61) and dequantisation uses
+  that fp16 value: ``(code - mid) * float(scale)`` (quant.py:68-73).
 """
 
 from __future__ import annotations
@@ -30,7 +30,7 @@ class QuantizedTensor:
 
 
 def _check(x: torch.Tensor, bits: int, group_size: int) -> None:
-    # Error types and messages mirror src/kvssd/quant.py:43-51.
+    # Error types and messages mirror src/kvssd/quant.py:17-25.
     if bits not in (2, 4):
         raise ValueError(f"bits must be 2 or 4, got {bits}")
     if group_size <= 0 or group_size % (8 // bits):

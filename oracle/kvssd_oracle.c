@@ -39,7 +39,7 @@
 /* ---------------------------------------------------------------- fp16 --- */
 
 /* IEEE binary16 -> binary32 (exact).  The reference stores scales as fp16
- * (src/kvssd/quant.py:87) and reads them with .float() (quant.py:98,
+ * (src/kvssd/quant.py:61) and reads them with .float() (quant.py:72,
  * backends/reference.py:31). */
 ORC_API float orc_f16_to_f32(uint16_t h) {
   uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
@@ -66,7 +66,7 @@ ORC_API float orc_f16_to_f32(uint16_t h) {
 
 /* binary32 -> binary16 with round-to-nearest-even, subnormals kept, overflow to
  * infinity: the semantics of torch's .to(torch.float16) used for the scales
- * (src/kvssd/quant.py:87). */
+ * (src/kvssd/quant.py:61). */
 ORC_API uint16_t orc_f32_to_f16(float f) {
   uint32_t x;
   memcpy(&x, &f, 4);
@@ -101,10 +101,10 @@ ORC_API uint16_t orc_f32_to_f16(float f) {
 
 /* --------------------------------------------------------- quantisation --- */
 
-/* Symmetric groupwise quantiser, restating src/kvssd/quant.py:75-91 in fp32:
- *   scale32 = max(|x|).clamp_min(1e-8) / (2^(bits-1)-1)       (quant.py:82)
- *   code    = clamp(round_half_even(x / scale32), -mid, pmax) + mid (quant.py:83-84)
- *   scale   = fp16(scale32)                                   (quant.py:87)
+/* Symmetric groupwise quantiser, restating src/kvssd/quant.py:49-65 in fp32:
+ *   scale32 = max(|x|).clamp_min(1e-8) / (2^(bits-1)-1)       (quant.py:56)
+ *   code    = clamp(round_half_even(x / scale32), -mid, pmax) + mid (quant.py:57-58)
+ *   scale   = fp16(scale32)                                   (quant.py:61)
  * x holds n_groups * group_size floats; codes one byte per element. */
 ORC_API void orc_quantize_groups(const float* x, int64_t n_groups, int group_size, int bits,
                                  uint8_t* codes, uint16_t* scales) {
@@ -130,7 +130,7 @@ ORC_API void orc_quantize_groups(const float* x, int64_t n_groups, int group_siz
   }
 }
 
-/* Low-bits-first packing along the last dim: src/kvssd/quant.py:54-63. */
+/* Low-bits-first packing along the last dim: src/kvssd/quant.py:28-37. */
 ORC_API void orc_pack_codes(const uint8_t* codes, int64_t n_codes, int bits, uint8_t* packed) {
   const int per = 8 / bits;
   for (int64_t b = 0; b < n_codes / per; ++b) {
@@ -159,11 +159,18 @@ static inline double dequant(const uint8_t* packed, const uint16_t* scales, int6
   return (double)(code - mid) * (double)orc_f16_to_f32(scales[row * groups + d / g]);
 }
 
+/* Rows of a block that take part for its count v: the rows Python's slice
+ * keys[index, :v] keeps in src/kvssd/backends/reference.py:38-40, i.e.
+ * min(v, BT) for v >= 0 and max(BT + v, 0) for v < 0. */
+static inline int slice_rows(int v, int bt) {
+  const int n = v < 0 ? bt + v : v;
+  return n < 0 ? 0 : (n > bt ? bt : n);
+}
+
 /* Decode attention over a packed batch: restates
  * ReferenceAttentionBackend.run (src/kvssd/backends/reference.py:22-50).
- *   - tokens are the first valid[b] rows of each block, blocks in batch order
- *     (reference.py:38-42); valid is clamped to [0, BT] (a negative count keeps
- *     no rows, as the CUDA kernel's loop bound does, csrc/fused_decode.cu:47);
+ *   - tokens are the rows keys[b, :valid[b]] of each block (slice_rows), blocks
+ *     in batch order (reference.py:36-42);
  *   - GQA map qh -> qh / (QH/KVH) (reference.py:45);
  *   - s = sm_scale * q.k, lse = logsumexp(s), out = softmax(s) @ V
  *     (reference.py:46-49).
@@ -185,8 +192,7 @@ ORC_API int orc_decode_attention(int qh, int kvh, int d, int nb, int bt, int bit
   for (int i = 0; i < nsel; ++i) {
     int b = block_table ? block_table[i] : i;
     if (b < 0 || b >= nb) return -1;
-    int v = valid[b];
-    total += v < 0 ? 0 : (v > bt ? bt : v);
+    total += slice_rows(valid[b], bt);
   }
 #ifdef _OPENMP
   if (threads > 0) omp_set_num_threads(threads);
@@ -202,8 +208,7 @@ ORC_API int orc_decode_attention(int qh, int kvh, int d, int nb, int bt, int bit
     int64_t n = 0;
     for (int i = 0; i < nsel; ++i) {
       int b = block_table ? block_table[i] : i;
-      int v = valid[b];
-      v = v < 0 ? 0 : (v > bt ? bt : v);
+      const int v = slice_rows(valid[b], bt);
       for (int t = 0; t < v; ++t) {
         int64_t row = ((int64_t)b * bt + t) * kvh + kv;
         double s = 0.0;
@@ -217,8 +222,7 @@ ORC_API int orc_decode_attention(int qh, int kvh, int d, int nb, int bt, int bit
     n = 0;
     for (int i = 0; i < nsel; ++i) {
       int b = block_table ? block_table[i] : i;
-      int v = valid[b];
-      v = v < 0 ? 0 : (v > bt ? bt : v);
+      const int v = slice_rows(valid[b], bt);
       for (int t = 0; t < v; ++t) {
         int64_t row = ((int64_t)b * bt + t) * kvh + kv;
         double p = exp(scores[n++] - mx);
@@ -234,7 +238,7 @@ ORC_API int orc_decode_attention(int qh, int kvh, int d, int nb, int bt, int bit
   return 0;
 }
 
-/* Exact merge of two normalised chunks: src/kvssd/attention.py:287-298
+/* Exact merge of two normalised chunks: src/kvssd/attention.py:91-102
  *   L = logaddexp(La, Lb); O = Oa e^(La-L) + Ob e^(Lb-L).
  * A chunk with L = -inf (no tokens) contributes nothing; two empty chunks give
  * O = 0, L = -inf (the result of attending over their empty union). */
@@ -260,7 +264,7 @@ ORC_API void orc_merge(int rows, int d, const float* oa, const float* la, const 
 /* ------------------------------------------------------------------ crc --- */
 
 /* Reflected CRC-32 (polynomial 0xEDB88320), the checksum zlib.crc32 computes
- * over each record payload (src/kvssd/format.py:214, :250). */
+ * over each record payload (src/kvssd/format.py:115, :151). */
 ORC_API uint32_t orc_crc32(const uint8_t* data, size_t n, uint32_t crc) {
   static uint32_t table[256];
   static int ready = 0;

@@ -88,7 +88,7 @@ def _ptr(a: np.ndarray | None) -> int | None:
 def quantize_np(x: np.ndarray, bits: int, group_size: int) -> tuple[np.ndarray, np.ndarray]:
     """Unpacked codes (uint8, x.shape) and fp16 scales ([..., D/g]).
 
-    Restates src/kvssd/quant.py:75-91 with numpy float32 arithmetic: IEEE
+    Restates src/kvssd/quant.py:49-65 with numpy float32 arithmetic: IEEE
     division, ``np.rint`` (round half to even, as ``torch.round``), then
     ``astype(float16)`` (round to nearest even) for the stored scale.
     """
@@ -114,7 +114,7 @@ def quantize_c(x: np.ndarray, bits: int, group_size: int) -> tuple[np.ndarray, n
 
 
 def pack_np(codes: np.ndarray, bits: int) -> np.ndarray:
-    """Low-bits-first packing along the last dim (src/kvssd/quant.py:54-63)."""
+    """Low-bits-first packing along the last dim (src/kvssd/quant.py:28-37)."""
     per = 8 // bits
     c = codes.astype(np.uint16).reshape(*codes.shape[:-1], -1, per)
     out = np.zeros(c.shape[:-1], dtype=np.uint16)
@@ -133,7 +133,7 @@ def unpack_np(packed: np.ndarray, bits: int, elements: int | None = None) -> np.
 
 
 def dequantize_np(codes: np.ndarray, scales: np.ndarray, bits: int, group_size: int) -> np.ndarray:
-    """(code - mid) * scale in float32 (src/kvssd/quant.py:94-99); exact."""
+    """(code - mid) * scale in float32 (src/kvssd/quant.py:68-73); exact."""
     mid = 1 << (bits - 1)
     g = codes.astype(np.float32).reshape(*codes.shape[:-1], codes.shape[-1] // group_size, group_size) - mid
     return (g * scales.astype(np.float32)[..., None]).reshape(codes.shape)
@@ -182,7 +182,7 @@ def select_recent_sink(available: list[int], sink: int, recent: int) -> list[int
 
 
 def record_bytes(kv_heads: int, head_dim: int, block_tokens: int, bits: int, group_size: int) -> int:
-    """CacheSpec.record_bytes (src/kvssd/format.py:139-157)."""
+    """CacheSpec.record_bytes (src/kvssd/format.py:53-58)."""
     scale_count = block_tokens * kv_heads * (head_dim // group_size)
     packed_count = block_tokens * kv_heads * head_dim * bits // 8
     payload = 2 * scale_count * 2 + 2 * packed_count
@@ -190,7 +190,7 @@ def record_bytes(kv_heads: int, head_dim: int, block_tokens: int, bits: int, gro
 
 
 def encode_record(layer, block, valid, bits, block_tokens, kv_heads, head_dim, group_size, ks, vs, kp, vp) -> bytes:
-    """Record v1 (src/kvssd/format.py:203-230): 52-byte header, payload
+    """Record v1 (src/kvssd/format.py:104-131): 52-byte header, payload
     Ks | Vs | Kc | Vc, zero padding to a 4096 multiple; CRC-32 of the payload."""
     payload = b"".join(
         np.ascontiguousarray(a).tobytes()
@@ -303,7 +303,7 @@ def attention(
 
 
 def merge(oa: np.ndarray, la: np.ndarray, ob: np.ndarray, lb: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """merge_attention_chunks (src/kvssd/attention.py:287-298) by the C oracle."""
+    """merge_attention_chunks (src/kvssd/attention.py:91-102) by the C oracle."""
     oa = np.ascontiguousarray(oa, dtype=np.float32)
     ob = np.ascontiguousarray(ob, dtype=np.float32)
     la = np.ascontiguousarray(la, dtype=np.float32)

@@ -83,3 +83,53 @@ def test_record_codec_sizes_and_argument_errors():
     assert lib.kvssd_hip_vllm_sizes(1 << 27, 4, 32, ctypes.byref(rec), ctypes.byref(scratch)) < 0  # > 16 MiB payload
     assert lib.kvssd_hip_vllm_encode(None, 3, 64, 4, 32, None, None, None, 0, None) < 0  # float64
     assert lib.kvssd_hip_vllm_decode(None, 64, 4, 32, 0, 0, None, None, None, 0, None) < 0
+
+
+def _need(msg: str) -> int:
+    m = re.search(r"need (\d+) bytes", msg)
+    assert m, msg
+    return int(m.group(1))
+
+
+@pytest.mark.parametrize("selected", [1, 33, 700])
+def test_num_selected_plans_the_same_splits_in_every_phase(selected):
+    # a table of `selected` ids out of 2048 blocks: the workspace query, the
+    # partials phase (table given) and the merge phase (no table pointer) agree
+    # on the split plan; none of these calls reaches a launch
+    lib = _native.load()
+    desc = _native.DecodeDesc(64, 8, 128, 2048, 128, 4, 32, 0, selected, 0, 0.1)
+    n = ctypes.c_size_t(0)
+    assert lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(n)) == 0
+    fake_table = ctypes.c_void_p(256)
+    rc = lib.kvssd_hip_decode_partials(ctypes.byref(desc), *([None] * 6), fake_table, None, 0, None)
+    assert rc < 0
+    need_partials = _need(_native.last_error())
+    rc = lib.kvssd_hip_decode_merge(ctypes.byref(desc), None, 0, None, None, None)
+    assert rc < 0
+    need_merge = _need(_native.last_error())
+    assert n.value == need_partials == need_merge
+    # the same count as a compacted batch of `selected` blocks plans alike
+    compact = _native.DecodeDesc(64, 8, 128, selected, 128, 4, 32, 0, 0, 0, 0.1)
+    m = ctypes.c_size_t(0)
+    assert lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(compact), ctypes.byref(m)) == 0
+    assert m.value == n.value
+
+
+def test_num_selected_without_a_table_is_an_argument_error():
+    lib = _native.load()
+    desc = _native.DecodeDesc(32, 8, 128, 64, 128, 4, 32, 0, 5, 0, 0.1)
+    fake = [ctypes.c_void_p(256)] * 6
+    work = ctypes.c_void_p(256)
+    rc = lib.kvssd_hip_decode_partials(ctypes.byref(desc), *fake, None, work, 1 << 30, None)
+    assert rc < 0 and "num_selected must be 0 when block_table is NULL" in _native.last_error()
+    rc = lib.kvssd_hip_fused_decode(ctypes.byref(desc), *fake, None, ctypes.c_void_p(256), ctypes.c_void_p(256),
+                                    work, 1 << 30, None)
+    assert rc < 0 and "num_selected must be 0" in _native.last_error()
+    desc.num_selected = -1
+    n = ctypes.c_size_t(0)
+    assert lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(n)) < 0
+    assert "num_selected must be >= 0" in _native.last_error()
+    # a table with no entries
+    desc.num_selected = 0
+    rc = lib.kvssd_hip_decode_partials(ctypes.byref(desc), *fake, ctypes.c_void_p(256), work, 1 << 30, None)
+    assert rc < 0 and "at least one block is required" in _native.last_error()

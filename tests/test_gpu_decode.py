@@ -66,7 +66,7 @@ def check(out, lse, ref_out, ref_lse, atol=ATOL, rtol=RTOL):
 def kernels_for(query, batch):
     """Every kernel that supports this shape ("general" always)."""
     names = []
-    for kernel in ("general", "mfma", "staged", "pairs"):
+    for kernel in ("general", "mfma", "staged"):
         try:
             HipAttentionBackend(kernel).kernel_for(query, batch)
         except ValueError:
@@ -235,7 +235,7 @@ def test_config_cpu_runnable_4096_tokens(cuda_device):
     scale = 1 / math.sqrt(128)
     ref_out, ref_lse = O.attention(q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, scale)
     query, batch = to_device(cuda_device, q.float().numpy(), pk, pv, sk, sv, valid, 4, 32, torch.float16)
-    assert kernels_for(query, batch) == ["general", "mfma", "staged", "pairs"]
+    assert kernels_for(query, batch) == ["general", "mfma", "staged"]
     for kernel in kernels_for(query, batch):
         out, lse = HipAttentionBackend(kernel).run(query, batch, scale)
         check(out, lse, ref_out, ref_lse)
@@ -279,7 +279,7 @@ def test_misaligned_buffers_use_general_kernel(cuda_device):
     out, lse = auto.run(query, moved, 0.1)
     assert auto.last_kernel == "general"
     check(out, lse, ref_out, ref_lse)
-    for kernel in ("mfma", "staged", "pairs"):
+    for kernel in ("mfma", "staged"):
         with pytest.raises(ValueError, match="aligned"):
             HipAttentionBackend(kernel).run(query, moved, 0.1)
 

@@ -32,7 +32,7 @@ def load(name: str) -> dict[str, np.ndarray]:
 def kernels_for(query, batch):
     """Every kernel that supports this shape ("general" always)."""
     names = []
-    for kernel in ("general", "mfma", "staged", "pairs"):
+    for kernel in ("general", "mfma", "staged"):
         try:
             HipAttentionBackend(kernel).kernel_for(query, batch)
         except ValueError:

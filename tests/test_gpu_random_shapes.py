@@ -1,8 +1,8 @@
 """Seeded sweep of decode shapes drawn from the whole supported domain.
 
 Each case draws kv heads, GQA ratio, head dim, group size, block size, block
-count, valid counts (including negative and oversized ones, which clamp to
-[0, block_tokens]), an optional block table (any order, repeats allowed), the
+count, valid counts (including oversized ones, which keep the whole block, and
+negative ones, which drop rows from the block's end as a Python slice does), an optional block table (any order, repeats allowed), the
 query dtype, the softmax scale and the value range, and runs every kernel that
 supports the shape against the CPU oracle at the contract tolerance
 (max-abs 2e-3, rel 1e-2).  The draws are fixed by the seed, so a failure names
@@ -50,7 +50,7 @@ def draw(seed: int) -> dict:
 
 def kernels_for(query, batch):
     names = []
-    for kernel in ("general", "mfma", "staged", "pairs"):
+    for kernel in ("general", "mfma", "staged"):
         try:
             HipAttentionBackend(kernel).kernel_for(query, batch)
         except ValueError:

@@ -258,16 +258,45 @@ def test_attention_block_table_empty_and_clamping():
     out, lse = O.attention(q, pk, pv, sk, sv, np.zeros(6, np.int32), 4, 32, 0.125)
     assert (out == 0).all() and np.isneginf(lse).all()
     big = np.full(6, 99, np.int32)
-    neg = valid.copy()
-    neg[2] = -5
     o1, _ = O.attention(q, pk, pv, sk, sv, big, 4, 32, 0.125)
     o2, _ = O.attention(q, pk, pv, sk, sv, np.full(6, 16, np.int32), 4, 32, 0.125)
     np.testing.assert_array_equal(o1, o2)
-    z = valid.copy()
-    z[2] = 0
-    o3, _ = O.attention(q, pk, pv, sk, sv, neg, 4, 32, 0.125)
-    o4, _ = O.attention(q, pk, pv, sk, sv, z, 4, 32, 0.125)
-    np.testing.assert_array_equal(o3, o4)
+
+
+def _sliced_attention(q, pk, pv, sk, sv, valid, bits, g, scale):
+    """float64 attention over the rows numpy's own slice ``x[b, :valid[b]]``
+    keeps: the rule of src/kvssd/backends/reference.py:38-40, applied by the
+    interpreter rather than restated."""
+    def deq(p, s):
+        codes = O.unpack_np(p, bits, p.shape[-1] * 8 // bits).astype(np.float64) - (1 << (bits - 1))
+        return codes * np.repeat(s.astype(np.float64), g, axis=-1)
+
+    k, v = deq(pk, sk), deq(pv, sv)
+    ks = np.concatenate([k[b, :n] for b, n in enumerate(valid.tolist())])
+    vs = np.concatenate([v[b, :n] for b, n in enumerate(valid.tolist())])
+    gq = q.shape[0] // k.shape[2]
+    out = np.zeros(q.shape)
+    lse = np.full(q.shape[0], -np.inf)
+    for h in range(q.shape[0]):
+        if len(ks) == 0:
+            continue
+        s = ks[:, h // gq] @ q[h].astype(np.float64) * scale
+        m = s.max()
+        w = np.exp(s - m)
+        out[h] = w @ vs[:, h // gq] / w.sum()
+        lse[h] = m + np.log(w.sum())
+    return out, lse
+
+
+@pytest.mark.parametrize("counts", [[16, 3, -5, 16, -16, 9], [-1, -20, 40, -15, 0, -3], [-16] * 6])
+def test_attention_negative_counts_follow_the_slice_rule(counts):
+    # a negative count drops rows from the end of its block, as keys[b, :v] does
+    q, pk, pv, sk, sv, _ = make_case(5, 8, 2, 64, 6, 16, 4, 32)
+    valid = np.array(counts, np.int32)
+    out, lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.125)
+    ref_out, ref_lse = _sliced_attention(q, pk, pv, sk, sv, valid, 4, 32, 0.125)
+    np.testing.assert_allclose(out, ref_out, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(lse, ref_lse, rtol=1e-6, atol=1e-6)
 
 
 def test_merge_split_anywhere_invariant():
