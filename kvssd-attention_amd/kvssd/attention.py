@@ -8,8 +8,8 @@ from collections.abc import Sequence
 import torch
 
 from .backends import AttentionBackend, PackedBatch, resolve_attention_backend
+from .backends.reference import ReferenceAttentionBackend
 from .format import PackedKVBlock
-from .quant import dequantize_tensor
 
 # The fused native kernel here is the HIP one.  ``require_cuda_kernel=True`` in the
 # reference means "the fused native kernel must run"; on ROCm that kernel is
@@ -24,17 +24,25 @@ def reference_attention(
     values: torch.Tensor,
     sm_scale: float | None = None,
 ) -> torch.Tensor:
-    """Decode attention with query [QH,D] and K/V [T,KVH,D], including GQA."""
+    """Decode attention with query [QH,D] and K/V [T,KVH,D], including GQA.
+
+    The reference's dense path (src/kvssd/attention.py:13-31): fp32 scores
+    scaled by ``sm_scale`` (default 1/sqrt(D)), softmax over the tokens, the
+    result cast to the query's dtype.  The query heads are grouped by the kv
+    head they read ([KVH, QH/KVH, D]), so each kv head's keys and values take
+    part in one batched product instead of being gathered per query head."""
     if query.ndim != 2 or keys.ndim != 3 or keys.shape != values.shape:
         raise ValueError("expected query [QH,D] and matching keys/values [T,KVH,D]")
     q_heads, dim = query.shape
-    if keys.shape[2] != dim or q_heads % keys.shape[1]:
+    _, kv_heads, key_dim = keys.shape
+    if key_dim != dim or q_heads % kv_heads:
         raise ValueError("head_dim mismatch or query heads not divisible by KV heads")
-    head_map = torch.arange(q_heads, device=query.device) // (q_heads // keys.shape[1])
-    scale = sm_scale if sm_scale is not None else 1.0 / math.sqrt(dim)
-    scores = torch.einsum("hd,thd->ht", query.float(), keys[:, head_map].float()) * scale
-    weights = torch.softmax(scores, dim=-1)
-    return torch.einsum("ht,thd->hd", weights, values[:, head_map].float()).to(query.dtype)
+    scale = 1.0 / math.sqrt(dim) if sm_scale is None else sm_scale
+    grouped = query.float().reshape(kv_heads, q_heads // kv_heads, dim)
+    k_t = keys.float().permute(1, 2, 0).contiguous()  # [KVH, D, T]
+    v = values.float().permute(1, 0, 2).contiguous()  # [KVH, T, D]
+    weights = torch.softmax(torch.matmul(grouped, k_t) * scale, dim=-1)
+    return torch.matmul(weights, v).reshape(q_heads, dim).to(query.dtype)
 
 
 def packed_attention_reference(
@@ -42,38 +50,53 @@ def packed_attention_reference(
     blocks: Sequence[PackedKVBlock],
     sm_scale: float | None = None,
 ) -> torch.Tensor:
+    """Packed blocks through the portable dequantize-then-attend backend
+    (src/kvssd/attention.py:34-47): each block contributes its first
+    ``valid_tokens`` rows, the result is cast to the query's dtype."""
     if not blocks:
         raise ValueError("at least one block is required")
-    keys = torch.cat([dequantize_tensor(b.key)[: b.valid_tokens] for b in blocks]).to(query.device)
-    values = torch.cat([dequantize_tensor(b.value)[: b.valid_tokens] for b in blocks]).to(query.device)
-    return reference_attention(query, keys, values, sm_scale)
+    scale = 1.0 / math.sqrt(query.shape[-1]) if sm_scale is None else sm_scale
+    batch = PackedBatch(*stack_blocks(blocks, query.device), blocks[0].key.bits, blocks[0].key.group_size)
+    out, _ = ReferenceAttentionBackend().run(query, batch, scale)
+    return out.to(query.dtype)
 
 
 def stack_blocks(blocks: Sequence[PackedKVBlock], device: torch.device) -> tuple[torch.Tensor, ...]:
-    """Coalesce blocks into PackedBatch tensors (kp, vp, ks, vs, valid) on ``device``."""
+    """PackedBatch tensors (packed K, packed V, scales K, scales V, valid) of
+    ``blocks`` on ``device`` (src/kvssd/attention.py:50-60).
+
+    Each array is assembled once in host memory, block by block, and crosses
+    to the device in one copy; the valid counts follow as one int32 tensor."""
     if not blocks:
         raise ValueError("at least one block is required")
     device = torch.device(device)
-    kwargs = {"device": device, "non_blocking": device.type == "cuda"}
-    return (
-        torch.stack([b.key.packed for b in blocks]).to(**kwargs),
-        torch.stack([b.value.packed for b in blocks]).to(**kwargs),
-        torch.stack([b.key.scales for b in blocks]).to(**kwargs),
-        torch.stack([b.value.scales for b in blocks]).to(**kwargs),
-        torch.tensor([b.valid_tokens for b in blocks], dtype=torch.int32, device=device),
+    fields = (
+        lambda b: b.key.packed,
+        lambda b: b.value.packed,
+        lambda b: b.key.scales,
+        lambda b: b.value.scales,
     )
+    arrays = []
+    for field in fields:
+        first = field(blocks[0])
+        host = torch.empty((len(blocks), *first.shape), dtype=first.dtype)
+        for row, block in enumerate(blocks):
+            host[row].copy_(field(block))
+        arrays.append(host.to(device))
+    counts = torch.tensor([int(b.valid_tokens) for b in blocks], dtype=torch.int32)
+    return (*arrays, counts.to(device))
 
 
 def native_backend_available() -> bool:
     """True when the fused HIP kernels can run on the current GPU."""
     try:
         resolve_attention_backend(NATIVE_BACKEND, torch.device("cuda"))
-        return True
     except RuntimeError:
         return False
+    return True
 
 
-# Name kept for API compatibility with the reference (src/kvssd/attention.py:63-68).
+# The reference's name for the same question (src/kvssd/attention.py:63-68).
 cuda_extension_available = native_backend_available
 
 
@@ -88,13 +111,12 @@ def fused_attention_tensors(
     group_size: int,
     sm_scale: float,
 ) -> tuple[torch.Tensor, torch.Tensor]:
-    """Low-level fused entry point returning normalized output and log-sum-exp statistics."""
-    backend = resolve_attention_backend(NATIVE_BACKEND, query.device)
-    return backend.run(
-        query,
-        PackedBatch(packed_k, packed_v, scales_k, scales_v, valid_tokens, bits, group_size),
-        sm_scale,
-    )
+    """(out fp32 [QH, D], lse fp32 [QH]) of the fused HIP kernels over one
+    PackedBatch: the low-level entry point of src/kvssd/attention.py:71-88,
+    which fails closed when the native backend is unavailable."""
+    native = resolve_attention_backend(NATIVE_BACKEND, query.device)
+    batch = PackedBatch(packed_k, packed_v, scales_k, scales_v, valid_tokens, bits, group_size)
+    return native.run(query, batch, sm_scale)
 
 
 def merge_attention_chunks(

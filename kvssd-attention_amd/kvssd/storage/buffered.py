@@ -1,76 +1,40 @@
-"""Portable positioned reads (reference: src/kvssd/storage/buffered.py:13-82)."""
+"""Buffered positioned reads through the page cache (the reference's
+``buffered`` backend, src/kvssd/storage/buffered.py:13-82).  Destinations may
+be page-locked: the loader reads records straight into the pipeline's
+staging rows."""
 
 from __future__ import annotations
 
-import os
-import threading
 from pathlib import Path
 
 import torch
 
 from ..format import BlockEntry
 from .base import StorageAvailability
+from .posix import PositionedFile, destination_view
 
 
-def host_buffer(size: int, pinned: bool) -> torch.Tensor:
-    """A CPU uint8 buffer; page-locked when asked and a GPU runtime is present."""
-    return torch.empty(size, dtype=torch.uint8, pin_memory=pinned and torch.cuda.is_available())
-
-
-class BufferedStorageBackend:
-    """Positioned reads into CPU tensors through the page cache."""
-
+class BufferedStorageBackend(PositionedFile):
     name = "buffered"
 
     def __init__(self, path: str | Path):
-        self.path = Path(path)
-        self._fd: int | None = None
-        self._lock = threading.Lock()
+        super().__init__(path)
 
     def probe(self) -> StorageAvailability:
-        if not self.path.is_file():
-            return StorageAvailability(self.name, False, False, True, f"data file does not exist: {self.path}")
-        return StorageAvailability(self.name, True, False, True, "portable buffered positioned reads")
+        if self.path.is_file():
+            return StorageAvailability(self.name, True, False, True, "portable buffered positioned reads")
+        return StorageAvailability(self.name, False, False, True, f"data file does not exist: {self.path}")
 
-    def _descriptor(self) -> int:
-        # One descriptor per backend, opened lazily under a lock so concurrent
-        # I/O workers never race to open duplicates.
-        with self._lock:
-            if self._fd is None:
-                self._fd = os.open(self.path, os.O_RDONLY | getattr(os, "O_BINARY", 0))
-            return self._fd
-
-    def allocate_buffer(
-        self,
-        size: int,
-        *,
-        pinned: bool = False,
-        device: torch.device | None = None,
-    ) -> torch.Tensor:
-        del device
-        return host_buffer(size, pinned)
+    def allocate_buffer(self, size: int, *, pinned: bool = False, device: torch.device | None = None) -> torch.Tensor:
+        return torch.empty(size, dtype=torch.uint8, pin_memory=bool(pinned) and torch.cuda.is_available())
 
     def read_into(self, entry: BlockEntry, destination: torch.Tensor) -> None:
         if destination.device.type != "cpu":
             raise ValueError("buffered backend requires a CPU destination tensor")
         if destination.dtype != torch.uint8 or destination.numel() < entry.length:
             raise ValueError("destination must be a sufficiently large uint8 tensor")
-        view = memoryview(destination[: entry.length].numpy())
-        fd = self._descriptor()
-        got = 0
-        while got < entry.length:
-            n = os.preadv(fd, [view[got:]], entry.offset + got)
-            if n <= 0:
-                break
-            got += n
+        got = self.read_exact(entry.offset, destination_view(destination, entry))
         if got != entry.length:
             raise EOFError(
-                f"short read for layer={entry.layer}, block={entry.block}: "
-                f"expected {entry.length}, got {got}"
+                f"short read for layer={entry.layer}, block={entry.block}: expected {entry.length}, got {got}"
             )
-
-    def close(self) -> None:
-        with self._lock:
-            if self._fd is not None:
-                os.close(self._fd)
-                self._fd = None

@@ -1,64 +1,51 @@
-"""Linux O_DIRECT reads into 4 KiB-aligned host buffers
-(reference: src/kvssd/storage/direct.py:14-94)."""
+"""O_DIRECT positioned reads that bypass the page cache (the reference's
+``direct`` backend, src/kvssd/storage/direct.py:24-94).
+
+O_DIRECT needs the file offset, the length and the destination address to be
+multiples of the block size (ALIGNMENT, 4 KiB); each is checked before the
+read with the reference's messages.  Buffers come from anonymous mmap (page
+aligned by construction).  They are pageable even when ``pinned=True`` is
+asked for: page-locked memory from the ROCm runtime is not a valid O_DIRECT
+target (the read fails with EFAULT), so the loader reads into these buffers
+and copies into its page-locked staging rows.
+"""
 
 from __future__ import annotations
 
 import os
 import sys
-import threading
 from pathlib import Path
 
 import torch
 
 from ..format import ALIGNMENT, BlockEntry
 from .base import StorageAvailability
+from .posix import PositionedFile, destination_view, page_aligned_buffer
 
 
-def aligned_host_buffer(size: int, *, pinned: bool = False) -> torch.Tensor:
-    """A CPU uint8 view of ``size`` bytes whose address is ALIGNMENT-aligned."""
-    owner = torch.empty(size + ALIGNMENT - 1, dtype=torch.uint8, pin_memory=pinned and torch.cuda.is_available())
-    shift = (-owner.data_ptr()) % ALIGNMENT
-    return owner[shift : shift + size]
-
-
-class DirectIOStorageBackend:
-    """Linux O_DIRECT positioned reads; offsets, lengths and addresses are checked."""
-
+class DirectIOStorageBackend(PositionedFile):
     name = "direct"
 
     def __init__(self, path: str | Path):
-        self.path = Path(path)
-        self._fd: int | None = None
-        self._lock = threading.Lock()
+        super().__init__(path, getattr(os, "O_DIRECT", 0))
 
     def probe(self) -> StorageAvailability:
+        def state(ok: bool, why: str) -> StorageAvailability:
+            return StorageAvailability(self.name, ok, True, True, why)
+
         if sys.platform != "linux" or not hasattr(os, "O_DIRECT"):
-            return StorageAvailability(self.name, False, True, True, "O_DIRECT requires Linux")
+            return state(False, "O_DIRECT requires Linux")
         if not self.path.is_file():
-            return StorageAvailability(self.name, False, True, True, f"data file does not exist: {self.path}")
+            return state(False, f"data file does not exist: {self.path}")
         try:
-            os.close(os.open(self.path, os.O_RDONLY | os.O_DIRECT))
+            fd = os.open(self.path, os.O_RDONLY | os.O_DIRECT)
         except OSError as exc:
-            return StorageAvailability(self.name, False, True, True, f"O_DIRECT open failed: {exc}")
-        return StorageAvailability(self.name, True, True, True, "Linux O_DIRECT positioned reads")
+            return state(False, f"O_DIRECT open failed: {exc}")
+        os.close(fd)
+        return state(True, "Linux O_DIRECT positioned reads")
 
-    def _descriptor(self) -> int:
-        with self._lock:
-            if self._fd is None:
-                self._fd = os.open(self.path, os.O_RDONLY | os.O_DIRECT)
-            return self._fd
-
-    def allocate_buffer(
-        self,
-        size: int,
-        *,
-        pinned: bool = False,
-        device: torch.device | None = None,
-    ) -> torch.Tensor:
-        # ROCm page-locked memory is not a valid O_DIRECT target (preadv fails
-        # with EFAULT), so direct-read buffers are always pageable.
-        del device, pinned
-        return aligned_host_buffer(size, pinned=False)
+    def allocate_buffer(self, size: int, *, pinned: bool = False, device: torch.device | None = None) -> torch.Tensor:
+        return page_aligned_buffer(size)
 
     def read_into(self, entry: BlockEntry, destination: torch.Tensor) -> None:
         if destination.device.type != "cpu" or destination.dtype != torch.uint8:
@@ -72,18 +59,11 @@ class DirectIOStorageBackend:
             )
         if destination.data_ptr() % ALIGNMENT:
             raise ValueError(
-                f"direct destination address must be {ALIGNMENT}-byte aligned; "
-                f"got address=0x{destination.data_ptr():x}"
+                f"direct destination address must be {ALIGNMENT}-byte aligned; got address=0x{destination.data_ptr():x}"
             )
-        got = os.preadv(self._descriptor(), [memoryview(destination[: entry.length].numpy())], entry.offset)
+        got = self.read_exact(entry.offset, destination_view(destination, entry))
         if got != entry.length:
             raise EOFError(
                 f"short direct read for layer={entry.layer}, block={entry.block}: "
                 f"offset={entry.offset}, expected={entry.length}, got={got}"
             )
-
-    def close(self) -> None:
-        with self._lock:
-            if self._fd is not None:
-                os.close(self._fd)
-                self._fd = None

@@ -1,31 +1,39 @@
-"""Pipeline on CPU: the reference's test (tests/test_pipeline.py:11-23) plus
-equality with the oracle over the selected blocks."""
+"""KVSSDPipeline.decode on the CPU: selection, bounded prefetch and the
+portable backend, end to end against the oracle over the selected blocks
+(the path of src/kvssd/pipeline.py:167-187 without a GPU)."""
+
+from __future__ import annotations
 
 import math
 from pathlib import Path
 
 import numpy as np
+import pytest
 import torch
 
 from kvssd.format import CacheSpec
 from kvssd.pipeline import KVSSDPipeline
-from kvssd.selectors import RecentSinkBlocks
+from kvssd.selectors import AllBlocks, RecentSinkBlocks
 from kvssd.store import KVCacheStore
 from oracle import oracle as O
 
 
-def test_cpu_end_to_end_with_selection(tmp_path: Path) -> None:
-    gen = torch.Generator().manual_seed(11)
-    shape = (1, 40, 2, 32)
-    keys, values = torch.randn(shape, generator=gen), torch.randn(shape, generator=gen)
-    store = KVCacheStore.create(tmp_path, keys, values, CacheSpec(1, 2, 32, block_tokens=8, bits=4, group_size=16))
-    query = torch.randn(4, 32, generator=gen)
-    with KVSSDPipeline(store, device="cpu", io_depth=2) as pipeline:
-        output = pipeline.decode(query, 0, RecentSinkBlocks(1, 2))
-    assert output.shape == (4, 32)
-    assert torch.isfinite(output).all()
-    pk, sk, valid = O.quantize_blocks(keys[0].numpy(), 4, 16, 8)
-    pv, sv, _ = O.quantize_blocks(values[0].numpy(), 4, 16, 8)
-    table = np.array(O.select_recent_sink(list(range(5)), 1, 2), np.int32)
-    expect, _ = O.attention(query.numpy(), pk, pv, sk, sv, valid, 4, 16, 1 / math.sqrt(32), block_table=table)
-    np.testing.assert_allclose(output.numpy(), expect, atol=2e-5, rtol=2e-5)
+@pytest.mark.parametrize("io_depth", [1, 2, 5])
+def test_decode_over_selections_matches_the_oracle(tmp_path: Path, io_depth: int):
+    gen = torch.Generator().manual_seed(70 + io_depth)
+    keys = torch.randn(2, 75, 2, 32, generator=gen)  # 10 blocks of 8, the last holding 3 tokens
+    values = torch.randn(2, 75, 2, 32, generator=gen)
+    store = KVCacheStore.create(tmp_path, keys, values, CacheSpec(2, 2, 32, block_tokens=8, bits=4, group_size=16))
+    query = torch.randn(4, 32, generator=gen, dtype=torch.float64)
+    with KVSSDPipeline(store, device="cpu", io_depth=io_depth) as pipe:
+        for layer in (0, 1):
+            pk, sk, valid = O.quantize_blocks(keys[layer].numpy(), 4, 16, 8)
+            pv, sv, _ = O.quantize_blocks(values[layer].numpy(), 4, 16, 8)
+            for sel in (AllBlocks(), RecentSinkBlocks(1, 2), RecentSinkBlocks(0, 1), RecentSinkBlocks(3, 0)):
+                out = pipe.decode(query, layer, sel)
+                assert out.shape == (4, 32) and out.dtype == torch.float64
+                ids = np.array(sel.select(list(range(10))), np.int32)
+                expect, _ = O.attention(query.float().numpy(), pk, pv, sk, sv, valid, 4, 16, 1 / math.sqrt(32),
+                                        block_table=ids)
+                np.testing.assert_allclose(out.numpy(), expect, atol=2e-5, rtol=2e-5)
+    store.close()

@@ -1,5 +1,8 @@
-"""Codec: the reference's tests (tests/test_quant.py:7-19) plus bit-exact
-agreement with the oracle's quantiser and packer."""
+"""The INT2/INT4 codec on the CPU: the error bound of the round trip, the
+argument checks of src/kvssd/quant.py:17-25, bit-exact agreement with the
+oracle's quantiser, and pack/unpack over every byte value."""
+
+from __future__ import annotations
 
 import numpy as np
 import pytest
@@ -9,23 +12,43 @@ from kvssd.quant import dequantize_tensor, pack_codes, quantize_tensor, unpack_c
 from oracle import oracle as O
 
 
-@pytest.mark.parametrize(("bits", "max_mae"), [(4, 0.12), (2, 0.65)])
-def test_quantization_round_trip(bits: int, max_mae: float) -> None:
-    x = torch.randn(3, 2, 128, generator=torch.Generator().manual_seed(1))
-    quantized = quantize_tensor(x, bits, group_size=32)
-    restored = dequantize_tensor(quantized)
-    assert restored.shape == x.shape
-    assert torch.mean(torch.abs(x - restored)).item() < max_mae
-    assert quantized.packed.numel() == x.numel() * bits // 8
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("group", [8, 32, 64])
+def test_round_trip_error_is_at_most_half_a_step(bits, group):
+    # inside the clamp range every value lands within half a quantisation step
+    # of its code; the one clamped code (-mid, never produced) is out of play
+    gen = torch.Generator().manual_seed(bits + group)
+    x = torch.randn(5, 3, 128, generator=gen) * torch.rand(5, 3, 1, generator=gen) * 3
+    q = quantize_tensor(x, bits, group)
+    back = dequantize_tensor(q)
+    assert back.shape == x.shape and back.dtype == torch.float32
+    assert q.packed.shape == (5, 3, 128 * bits // 8) and q.scales.shape == (5, 3, 128 // group)
+    step = q.scales.float().repeat_interleave(group, dim=-1)
+    # fp16 rounding of the stored scale moves a code by at most pmax * 2^-11 steps
+    slack = (2 ** (bits - 1) - 1) * 2.0**-11 * step + 1e-6
+    assert torch.all((x - back).abs() <= step / 2 + slack)
 
 
-def test_rejects_invalid_layout() -> None:
-    with pytest.raises(ValueError, match="divisible"):
+@pytest.mark.parametrize(("bits", "mae_bound"), [(4, 0.12), (2, 0.65)])
+def test_mean_error_on_unit_normal_data(bits, mae_bound):
+    # the reference's published bounds for N(0, 1) values in groups of 32
+    for seed in range(4):
+        x = torch.randn(16, 8, 128, generator=torch.Generator().manual_seed(seed))
+        err = (dequantize_tensor(quantize_tensor(x, bits, 32)) - x).abs().mean().item()
+        assert err < mae_bound
+
+
+def test_argument_checks():
+    with pytest.raises(ValueError, match="divisible by group_size"):
         quantize_tensor(torch.randn(2, 31), 4, group_size=16)
-    with pytest.raises(ValueError, match="bits"):
+    with pytest.raises(ValueError, match="bits must be 2 or 4"):
         quantize_tensor(torch.randn(2, 32), 3, group_size=16)
-    with pytest.raises(TypeError):
+    with pytest.raises(ValueError, match="pack-aligned"):
+        quantize_tensor(torch.randn(2, 32), 2, group_size=2)
+    with pytest.raises(TypeError, match="floating point"):
         quantize_tensor(torch.ones(2, 32, dtype=torch.int32), 4, group_size=16)
+    with pytest.raises(ValueError, match="byte aligned"):
+        pack_codes(torch.zeros(3, dtype=torch.uint8), 2)
 
 
 @pytest.mark.parametrize("bits", [2, 4])

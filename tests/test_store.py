@@ -1,6 +1,9 @@
-"""Store, record format and loader: the reference's tests
-(tests/test_store.py:20-59) plus byte equality with the oracle's record."""
+"""Store, record format, storage backends and loader on the CPU: padding,
+CRC and header checks of decode_record (src/kvssd/format.py:134-177), the
+prefetcher's slot reuse and descriptor lifecycle, byte equality with the
+oracle's records, and the record-native reads the GPU pipeline uses."""
 
+import os
 from pathlib import Path
 
 import numpy as np
@@ -22,45 +25,74 @@ def make_store(path: Path, bits: int = 4, storage=None) -> tuple[KVCacheStore, t
     return KVCacheStore.create(path, keys, values, spec, storage), keys, values
 
 
-def test_store_round_trip_and_padding(tmp_path: Path) -> None:
+def test_padded_tail_block_decodes_to_zeros(tmp_path: Path) -> None:
+    # 19 tokens in blocks of 8: blocks 0, 1 full, block 2 holds 3 tokens and
+    # 5 zero rows (src/kvssd/store.py:47-53); every record starts on a 4 KiB
+    # boundary; the stored codes are exactly the oracle's
     store, keys, _ = make_store(tmp_path)
-    block = store.read(1, 2)
-    assert block.valid_tokens == 3
-    restored = dequantize_tensor(block.key)
-    assert torch.mean(torch.abs(restored[:3] - keys[1, 16:])).item() < 0.15
-    assert torch.count_nonzero(restored[3:]) == 0
-    assert all(entry.offset % 4096 == 0 for entry in store.manifest.entries)
+    assert [store.read(1, b).valid_tokens for b in range(3)] == [8, 8, 3]
+    assert all(e.offset % 4096 == 0 and e.length % 4096 == 0 for e in store.manifest.entries)
+    tail = store.read(1, 2)
+    back = dequantize_tensor(tail.key)
+    assert torch.count_nonzero(back[3:]) == 0
+    assert torch.count_nonzero(tail.key.scales[3:]) == 0
+    pk, sk, _ = O.quantize_blocks(keys[1].numpy(), 4, 16, 8)
+    assert np.array_equal(tail.key.packed.numpy(), pk[2])
+    assert np.array_equal(tail.key.scales.numpy().view(np.uint16), sk[2].view(np.uint16))
 
 
-def test_crc_detects_corruption(tmp_path: Path) -> None:
+@pytest.mark.parametrize("at", [52, 53, 52 + 70, 52 + 300, 52 + 639])  # payload: 640 bytes after the header
+def test_any_payload_byte_flip_fails_the_crc(tmp_path: Path, at: int) -> None:
     store, _, _ = make_store(tmp_path)
-    entry = store.entry(0, 0)
-    data_path = tmp_path / "blocks.kvssd"
-    with data_path.open("r+b") as f:
-        f.seek(entry.offset + 80)
-        old = f.read(1)
-        f.seek(entry.offset + 80)
-        f.write(bytes([old[0] ^ 0xFF]))
-    with pytest.raises(IOError, match="CRC"):
-        store.read(0, 0)
+    entry = store.entry(1, 1)
+    with (tmp_path / "blocks.kvssd").open("r+b") as f:
+        f.seek(entry.offset + at)
+        byte = f.read(1)[0]
+        f.seek(entry.offset + at)
+        f.write(bytes([byte ^ 0x10]))
+    with pytest.raises(IOError, match="CRC mismatch for layer=1, block=1"):
+        store.read(1, 1)
+    store.read(1, 0)  # neighbours are untouched
 
 
-def test_async_loader_does_not_alias_recycled_slots(tmp_path: Path) -> None:
+def test_corrupt_header_is_a_value_error(tmp_path: Path) -> None:
     store, _, _ = make_store(tmp_path)
-    with AsyncBlockLoader(store, depth=2, pinned=False) as loader:
-        blocks = list(loader.iter_blocks(0, [0, 1, 2]))
-    snapshots = [x.key.packed.clone() for x in blocks]
-    assert [x.block for x in blocks] == [0, 1, 2]
-    assert all(torch.equal(x.key.packed, expected) for x, expected in zip(blocks, snapshots))
-    direct = [store.read(0, i) for i in range(3)]
-    assert all(torch.equal(a.value.packed, b.value.packed) for a, b in zip(blocks, direct))
+    with (tmp_path / "blocks.kvssd").open("r+b") as f:
+        f.seek(store.entry(0, 2).offset)
+        f.write(b"KVSSD002")
+    with pytest.raises(ValueError, match="invalid KVSSD record header"):
+        store.read(0, 2)
 
 
-def test_parallel_reader_closes_its_single_descriptor(tmp_path: Path) -> None:
+def test_prefetched_blocks_survive_slot_reuse(tmp_path: Path) -> None:
+    # one slot, so every block after the first is read into recycled memory;
+    # blocks already handed out must keep their own bytes
     store, _, _ = make_store(tmp_path)
-    with AsyncBlockLoader(store, depth=3, pinned=False) as loader:
-        list(loader.iter_blocks(0, [0, 1, 2]))
+    order = [2, 0, 1, 1, 0, 2]
+    with AsyncBlockLoader(store, depth=1, pinned=False) as loader:
+        held = list(loader.iter_blocks(0, order))
+    assert [b.block for b in held] == order
+    for b in held:
+        fresh = store.read(0, b.block)
+        assert b.valid_tokens == fresh.valid_tokens
+        for mine, theirs in ((b.key, fresh.key), (b.value, fresh.value)):
+            assert torch.equal(mine.packed, theirs.packed) and torch.equal(mine.scales, theirs.scales)
+
+
+def _open_descriptors() -> int:
+    return len(os.listdir("/proc/self/fd"))
+
+
+@pytest.mark.skipif(not os.path.isdir("/proc/self/fd"), reason="needs /proc/self/fd")
+@pytest.mark.parametrize("storage", ["buffered", "direct"])
+def test_concurrent_readers_share_one_descriptor(tmp_path: Path, storage: str) -> None:
+    before = _open_descriptors()
+    store, _, _ = make_store(tmp_path, storage=storage)
+    with AsyncBlockLoader(store, depth=4, pinned=False) as loader:
+        list(loader.iter_blocks(1, [0, 1, 2, 0, 1, 2]))
+        assert _open_descriptors() <= before + 1
     store.close()
+    assert _open_descriptors() == before
     (tmp_path / "blocks.kvssd").unlink()
 
 
