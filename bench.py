@@ -11,18 +11,21 @@ Infinity Cache cannot serve repeats.
 
 Output: one JSON line.  ``value`` is packed-KV GB/s over the whole step
 (algorithmic bytes / step time, the K steps timed back to back with events
-only at the two ends, after W untimed steps: 2000 by default, ~70 ms of load,
-since the GPU needs tens of milliseconds of work to reach its steady clocks
-and a short warmup reads ~8% slow); ``roofline.achieved`` is the same bytes over the
+only at the two ends, after W untimed warm-up steps).  Before the warm-up the
+bench runs untimed back-to-back steps for ``--settle-ms`` (50 ms by default,
+reported in ``settle``): an idle GPU needs tens of milliseconds of load to
+reach the clocks a continuous decode runs at, and a timed region that starts
+inside that ramp reads ~5-8% slow.  ``roofline.achieved`` is the same bytes over the
 dominant (split) kernel's average duration: a second pass launches the split
 kernel alone K times back to back between two HIP events on its stream.
 ``step_us`` gives p10 / p50 / p90 of single steps (an event pair around each).
 ``pipeline`` times the public Python path, ``KVSSDPipeline.decode`` on layers
 resident in HBM (selection, argument checks, allocation and the fp16 cast
 included), over a store of the workload's shape written to a temporary
-directory.  ``cpu_baseline`` is the CPU oracle (a plain-C port of the reference's
-dequantise-then-attend path) timed on this host's cores over a bounded sample
-of the same workload.
+directory.  ``cpu_baseline`` is the reference's CPU decode (the portable
+``reference`` backend: torch on all host cores) timed over a bounded sample of
+the same blocks, with the HIP result over that sample checked against it at
+the contract tolerance (``gpu_check``) and the C oracle's time beside it.
 
 ``--workload int4_gqa_1m_host_staged`` times the other regime: 1,048,576
 tokens whose raw records sit in page-locked host memory and stream to the GPU
@@ -181,42 +184,90 @@ def pipeline_leg(torch, dev, tokens: int, bits: int, qh: int, sel, steps: int, w
     }
 
 
-def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 20.0):
-    """Time the CPU oracle on a bounded sample of the same workload."""
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 4.0, gpu_run=None):
+    """The reference's CPU decode (ReferenceAttentionBackend.run: dequantise in
+    fp32, gather the GQA heads, softmax, on torch's CPU threads) timed on this
+    host's cores over a sample of the workload's blocks: 1 warm-up and 3 timed
+    runs, the median reported.  ``gpu_run(ids)`` gives the HIP result over the
+    same sample, checked here against the CPU result at the contract tolerance.
+    The C oracle (float64, OpenMP) over the same sample is a second figure."""
     import numpy as np
 
+    from kvssd.backends import PackedBatch
+    from kvssd.backends.reference import ReferenceAttentionBackend
     from oracle import oracle as O
 
-    threads = O.cpu_count()
-    pk, pv = cache["pk"].cpu().numpy(), cache["pv"].cpu().numpy()
-    sk, sv = cache["sk"].cpu().numpy(), cache["sv"].cpu().numpy()
-    va = valid.cpu().numpy()
-    q = query.float().cpu().numpy()
-    ids = np.arange(pk.shape[0], dtype=np.int32) if table is None else np.asarray(table, np.int32)
-    sample = ids
-    # calibrate on a slice, then size the sample to ~budget/3 seconds per run
-    probe = ids[: max(1, min(len(ids), 16))]
-    t0 = time.perf_counter()
-    O.attention(q, pk, pv, sk, sv, va, bits, GROUP, 1 / math.sqrt(HEAD_DIM), block_table=probe, threads=threads)
-    per_block = (time.perf_counter() - t0) / len(probe)
-    n = int(max(1, min(len(ids), (budget_s / 3) / max(per_block, 1e-9))))
-    sample = ids[:n]
-    times = []
-    for _ in range(3):
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    threads = torch.get_num_threads()
+    host = {k: t.cpu() for k, t in cache.items()}
+    va = valid.cpu()
+    q = query.cpu()
+    ids = list(range(host["pk"].shape[0])) if table is None else list(table)
+    scale = 1 / math.sqrt(HEAD_DIM)
+    backend = ReferenceAttentionBackend()
+
+    def run(sample):
+        idx = torch.tensor(sample, dtype=torch.long)
+        batch = PackedBatch(*(host[k].index_select(0, idx) for k in ("pk", "pv", "sk", "sv")), va[idx], bits, GROUP)
         t0 = time.perf_counter()
-        O.attention(q, pk, pv, sk, sv, va, bits, GROUP, 1 / math.sqrt(HEAD_DIM), block_table=sample, threads=threads)
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
+        out, lse = backend.run(q, batch, scale)
+        return time.perf_counter() - t0, out, lse
+
+    # size the sample from a 16-block probe so a run takes about budget_s
+    per_block = run(ids[: min(16, len(ids))])[0] / min(16, len(ids))
+    n = int(max(1, min(len(ids), budget_s / max(per_block, 1e-9))))
+    sample = ids[:n]
+    run(sample)  # warm-up
+    timed = [run(sample) for _ in range(3)]
+    t, out, lse = sorted(timed, key=lambda r: r[0])[1]
     nbytes = alg_bytes(len(sample), bits)
-    return {
-        "value": round(nbytes / t / 1e9, 3),
+    result = {
+        "value": round(nbytes / t / 1e9, 4),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{len(sample)} of {len(ids)} blocks of the same packed batch, median of 3 runs "
-        f"({t * 1e3:.1f} ms each; full step extrapolates to {t * len(ids) / len(sample) * 1e3:.1f} ms)",
+        "sample": f"{len(sample)} of {len(ids)} blocks of the same packed batch "
+        f"(ReferenceAttentionBackend.run on CPU tensors), median of 3 runs after 1 warm-up: {t * 1e3:.1f} ms each, "
+        f"a full step extrapolates to {t * len(ids) / len(sample) * 1e3:.1f} ms",
         "ms_per_full_step": round(t * len(ids) / len(sample) * 1e3, 3),
+        "os_cpu_count": cores,
+        "torch_threads": threads,
+        "cpu_model": cpu_model(),
     }
+    if gpu_run is not None:
+        g_out, g_lse = gpu_run(sample)
+        d_out = float((g_out.cpu() - out).abs().max())
+        d_lse = float((g_lse.cpu() - lse).abs().max())
+        ok = bool(torch.allclose(g_out.cpu(), out, atol=2e-3, rtol=1e-2) and
+                  torch.allclose(g_lse.cpu(), lse, atol=2e-3, rtol=1e-2))
+        result["gpu_check"] = {"max_abs_out": d_out, "max_abs_lse": d_lse, "tolerance": "atol 2e-3, rtol 1e-2",
+                               "blocks": len(sample), "ok": ok}
+    # the C restatement (float64, OpenMP) over the same sample
+    c_threads = min(cores, 64)
+    arr = {k: v.numpy() for k, v in host.items()}
+    sel = np.asarray(sample, np.int32)
+    O.attention(q.float().numpy(), arr["pk"], arr["pv"], arr["sk"], arr["sv"], va.numpy(), bits, GROUP, scale,
+                block_table=sel, threads=c_threads)
+    t0 = time.perf_counter()
+    O.attention(q.float().numpy(), arr["pk"], arr["pv"], arr["sk"], arr["sv"], va.numpy(), bits, GROUP, scale,
+                block_table=sel, threads=c_threads)
+    tc = time.perf_counter() - t0
+    result["c_port"] = {"value": round(nbytes / tc / 1e9, 4), "unit": "GB/s", "threads": c_threads,
+                        "ms_per_full_step": round(tc * len(ids) / len(sample) * 1e3, 3)}
+    return result
 
 
 def copy_calibration(torch, dev, nbytes: int, steps: int, warmup: int) -> int:
@@ -512,6 +563,11 @@ def host_staged(torch, dev, args) -> int:
         "records_ok": ok,
     }
     print(json.dumps(line), flush=True)
+    # release the ring, its streams and the page-locked records while the
+    # runtime is fully up, not in interpreter teardown
+    torch.cuda.synchronize()
+    del stager, fill, host, pinned, transfers, compute
+    torch.cuda.empty_cache()
     return 0
 
 
@@ -523,13 +579,18 @@ def main() -> int:
         "--warmup",
         type=int,
         default=None,
-        help="untimed steps first (default 2000 for the decode workloads: ~70 ms of load, which the GPU "
-        "needs to reach its steady clocks; 20 otherwise)",
+        help="untimed warm-up steps before the timed ones (default 20)",
     )
     ap.add_argument("--workload", default="int4_gqa_128k", choices=sorted(WORKLOADS) + sorted(HOST_STAGED) + sorted(CODEC))
     ap.add_argument("--kernel", default="auto", choices=["auto", "general", "mfma", "staged"])
     ap.add_argument("--copies", type=int, default=0, help="distinct KV copies rotated across steps (0 = auto)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument(
+        "--settle-ms",
+        type=float,
+        default=50.0,
+        help="wall time of untimed back-to-back decode steps before the warm-up steps (clock settle; 0 = none)",
+    )
     ap.add_argument(
         "--no-pipeline", action="store_true", help="skip the KVSSDPipeline.decode leg (decode workloads)"
     )
@@ -543,7 +604,7 @@ def main() -> int:
     )
     args = ap.parse_args()
     if args.warmup is None:
-        args.warmup = 2000 if args.workload in WORKLOADS and not args.copy_calibration else 20
+        args.warmup = 20
     if args.gpus != 1:
         print(
             "bench.py measures one GPU only: the library has no multi-GPU path "
@@ -620,8 +681,27 @@ def main() -> int:
         if rc:
             _native.check(rc, "decode")
 
+    # clock settle (disclosed in the line): back-to-back decode steps for
+    # --settle-ms of wall time before the W warm-up steps, so that the timed
+    # steps see the clocks a continuous decode runs at, not the power-up ramp
+    # of an idle GPU
+    settle_steps = 0
+    if args.settle_ms > 0:
+        t_end = time.perf_counter() + args.settle_ms / 1e3
+        while time.perf_counter() < t_end:
+            for _ in range(64):
+                step(settle_steps)
+                settle_steps += 1
+            torch.cuda.synchronize()
     for i in range(args.warmup):
         step(i)
+    torch.cuda.synchronize()
+    # host enqueue cost alone: K launches with nothing waited for (behind the
+    # queue the warm-up left, so the GPU never starves the measurement)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    enqueue_us = (time.perf_counter() - t0) / args.steps * 1e6
     torch.cuda.synchronize()
     # timed region: K back-to-back decode steps, events only at its two ends
     start = torch.cuda.Event(enable_timing=True)
@@ -654,7 +734,7 @@ def main() -> int:
 
     gbps = nbytes / (ms_per_step * 1e-3) / 1e9
     achieved = nbytes / (kern_avg * 1e-3) / 1e9
-    # quick numerical sanity on the last step's output against the portable path
+    # the output is compared with the CPU reference in the cpu_baseline leg
     ok = bool(torch.isfinite(out).all().item())
 
     traffic = None
@@ -705,6 +785,9 @@ def main() -> int:
             "kernel": f"decode_{kernel_name}",
         },
         "host_wall_ms_per_step": round(wall / args.steps * 1e3, 4),
+        "host_enqueue_us_per_step": round(enqueue_us, 2),
+        "settle": {"ms": args.settle_ms, "steps": settle_steps,
+                   "what": "untimed back-to-back decode steps before the W warm-up steps"},
         "finite": ok,
     }
     if not args.no_pipeline:
@@ -712,7 +795,14 @@ def main() -> int:
         layers = max(1, min(4, math.ceil(1.2e9 / alg_bytes(nb, bits))))
         line["pipeline"] = pipeline_leg(torch, dev, tokens, bits, qh, sel, args.steps, args.warmup, layers)
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(torch, query, {k: batches[0].__dict__[n] for k, n in (("pk", "packed_k"), ("pv", "packed_v"), ("sk", "scales_k"), ("sv", "scales_v"))}, valid, bits, table)
+        def gpu_run(ids):
+            out, lse = backend.run(query, batches[0], scale, block_table=ids)
+            torch.cuda.synchronize()
+            return out, lse
+
+        arrays = {k: getattr(batches[0], n) for k, n in
+                  (("pk", "packed_k"), ("pv", "packed_v"), ("sk", "scales_k"), ("sv", "scales_v"))}
+        line["cpu_baseline"] = cpu_baseline(torch, query, arrays, valid, bits, table, gpu_run=gpu_run)
     print(json.dumps(line), flush=True)
     return 0
 

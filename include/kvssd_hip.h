@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KVSSD_HIP_ABI_VERSION 3
+#define KVSSD_HIP_ABI_VERSION 4
 
 /* Query element types accepted by kvssd_hip_fused_decode (the reference
  * dispatches fp32/fp64/fp16/bf16 queries: csrc/fused_decode.cu:131-133). */

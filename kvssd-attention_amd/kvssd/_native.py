@@ -10,13 +10,16 @@ the library.  Loading fails loudly; nothing falls back to another path.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch  # noqa: F401  (must precede the library load; see module docstring)
 
-LIB_PATH = Path(__file__).resolve().parent / "libkvssd_hip.so"
-ABI_VERSION = 3
+# The in-tree build; KVSSD_HIP_LIBRARY names another build of the same ABI
+# (an instrumented one, say) for the whole process.
+LIB_PATH = Path(os.environ.get("KVSSD_HIP_LIBRARY") or Path(__file__).resolve().parent / "libkvssd_hip.so").resolve()
+ABI_VERSION = 4
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_GENERAL, KERNEL_MFMA, KERNEL_STAGED = 0, 1, 2, 3
@@ -90,19 +93,33 @@ class NativeError(RuntimeError):
     """A runtime failure reported by libkvssd_hip (positive status)."""
 
 
-def load() -> ctypes.CDLL:
-    """Load and type the library once; raises RuntimeError when it is absent or stale."""
-    global _lib, _load_error
+_loaded_from: Path | None = None
+
+
+def load(path: str | Path | None = None) -> ctypes.CDLL:
+    """Load and type the library once; raises RuntimeError when it is absent
+    or stale, and when a different build is asked for after one was loaded.
+
+    One process holds one build: two builds of the library carry the same
+    translation-unit ids (``__hip_cuid_*``) for their device code, and a
+    process that mapped two of them crashed at its first launches."""
+    global _lib, _load_error, _loaded_from
+    want = LIB_PATH if path is None else Path(path).resolve()
     with _lock:
         if _lib is not None:
+            if want != _loaded_from:
+                raise RuntimeError(
+                    f"libkvssd_hip is already loaded from {_loaded_from}; one process holds one build "
+                    f"(asked for {want}); run the other build in its own process"
+                )
             return _lib
-        if not LIB_PATH.exists():
-            _load_error = f"{LIB_PATH.name} is not built; run python kvssd-attention_amd/csrc/build.py"
+        if not want.exists():
+            _load_error = f"{want.name} is not built; run python kvssd-attention_amd/csrc/build.py"
             raise RuntimeError(_load_error)
         try:
-            lib = ctypes.CDLL(str(LIB_PATH))
+            lib = ctypes.CDLL(str(want))
         except OSError as exc:
-            _load_error = f"cannot load {LIB_PATH}: {exc}"
+            _load_error = f"cannot load {want}: {exc}"
             raise RuntimeError(_load_error) from exc
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(lib, name)
@@ -110,9 +127,9 @@ def load() -> ctypes.CDLL:
             fn.argtypes = args
         version = lib.kvssd_hip_abi_version()
         if version != ABI_VERSION:
-            _load_error = f"{LIB_PATH.name} ABI {version} != expected {ABI_VERSION}; rebuild it"
+            _load_error = f"{want.name} ABI {version} != expected {ABI_VERSION}; rebuild it"
             raise RuntimeError(_load_error)
-        _lib = lib
+        _lib, _loaded_from = lib, want
         return lib
 
 

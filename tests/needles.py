@@ -73,11 +73,15 @@ def needle_keys(q: np.ndarray, kv_heads: int, scale: float, target: float = 10.0
     return keys
 
 
-def needle_values(n: int, kv_heads: int, d: int, amp: float, rng: np.random.Generator) -> np.ndarray:
-    """[n, KVH, D] values: +-amp in one random dim per (needle, kv head)."""
+def needle_values(n: int, kv_heads: int, d: int, amp: float, rng: np.random.Generator, run: int = 1) -> np.ndarray:
+    """[n, KVH, D] values: +-amp in one random dim per (needle, kv head).
+    ``run`` consecutive needles share the dim and the sign (``run`` = 4: the
+    needles of one segment), so that dropping them moves one dim by
+    run * amp / N instead of spreading amp / N over ``run`` dims."""
     v = np.zeros((n, kv_heads, d), np.float32)
-    dims = rng.integers(0, d, (n, kv_heads))
-    signs = rng.choice([-1.0, 1.0], (n, kv_heads)).astype(np.float32)
+    groups = -(-n // run)
+    dims = np.repeat(rng.integers(0, d, (groups, kv_heads)), run, axis=0)[:n]
+    signs = np.repeat(rng.choice([-1.0, 1.0], (groups, kv_heads)).astype(np.float32), run, axis=0)[:n]
     v[np.arange(n)[:, None], np.arange(kv_heads)[None, :], dims] = signs * amp
     return v
 

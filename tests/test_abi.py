@@ -133,3 +133,13 @@ def test_num_selected_without_a_table_is_an_argument_error():
     desc.num_selected = 0
     rc = lib.kvssd_hip_decode_partials(ctypes.byref(desc), *fake, ctypes.c_void_p(256), work, 1 << 30, None)
     assert rc < 0 and "at least one block is required" in _native.last_error()
+
+
+def test_a_second_build_is_refused_in_the_same_process(tmp_path):
+    lib = _native.load()
+    assert _native.load(_native.LIB_PATH) is lib
+    other = tmp_path / "libkvssd_hip_other.so"
+    other.write_bytes(_native.LIB_PATH.read_bytes())
+    with pytest.raises(RuntimeError, match="one process holds one build"):
+        _native.load(other)
+    assert _native.load() is lib

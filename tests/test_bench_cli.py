@@ -18,7 +18,7 @@ def test_more_than_one_gpu_exits_with_a_message():
     assert proc.stdout == ""
 
 
-def test_help_names_the_workloads_and_the_warmup_default():
+def test_help_names_the_workloads_and_the_warmup_and_settle_defaults():
     proc = run_bench("--help")
     assert proc.returncode == 0
     for name in (
@@ -26,4 +26,6 @@ def test_help_names_the_workloads_and_the_warmup_default():
         "int4_gqa_1m_host_staged",
     ):
         assert name in proc.stdout
-    assert "2000" in proc.stdout
+    text = " ".join(proc.stdout.split())
+    assert "(default 20)" in text
+    assert "--settle-ms" in text and "(clock settle; 0 = none)" in text

@@ -104,9 +104,10 @@ def test_needles_eight_kv_heads_per_workgroup(cuda_device, bits, qh, kvh):
 
 def test_needles_host_staged_1m_tokens(cuda_device):
     # the 1,048,576-token host-staged stream: needles planted in the device
-    # K/V before the records are encoded; one needle moves the output by less
-    # than the tolerance here (131,072 needles per kv head), so the controls
-    # are one block and one 32-token segment
+    # K/V before the records are encoded.  With 131,072 needles per kv head one
+    # needle moves the output by less than the tolerance, so the four needles
+    # of a segment share their dim and sign (a dropped segment moves one dim by
+    # 4 amp / N) and the controls are one block and one 32-token segment
     from kvssd import records_hip as R
     from kvssd.staging import HostRecords, RecordStager
 
@@ -122,7 +123,7 @@ def test_needles_host_staged_1m_tokens(cuda_device):
     rows = torch.from_numpy(bb * 128 + tt).to(dev)
     nk = torch.from_numpy(N.needle_keys(q16.float().numpy(), 8, SCALE)).to(dev).half()
     keys[rows] = nk[None].expand(len(bb), 8, 128)
-    values[rows] = torch.from_numpy(N.needle_values(len(bb), 8, 128, 512.0, rng)).to(dev).half()
+    values[rows] = torch.from_numpy(N.needle_values(len(bb), 8, 128, 1024.0, rng, run=4)).to(dev).half()
     records, _ = R.encode_records(keys, values, spec, layer=0)
     del keys, values
     pinned = torch.empty(records.shape, dtype=torch.uint8, pin_memory=True)

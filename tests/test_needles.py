@@ -64,3 +64,12 @@ def test_moving_rows_to_the_end_removes_exactly_those_rows():
     out2, lse2 = N.oracle(q, [pk, pv, sk, sv], v2, 4)
     np.testing.assert_array_equal(out, out2)
     np.testing.assert_array_equal(lse, lse2)
+
+
+def test_segment_runs_share_dim_and_sign():
+    rng = np.random.default_rng(5)
+    v = N.needle_values(10, 3, 16, 8.0, rng, run=4)
+    nz = [np.flatnonzero(v[i, 1]) for i in range(10)]
+    assert all(len(x) == 1 for x in nz)
+    for a, b in ((0, 3), (4, 7), (8, 9)):
+        assert nz[a][0] == nz[b][0] and v[a, 1, nz[a][0]] == v[b, 1, nz[b][0]]
