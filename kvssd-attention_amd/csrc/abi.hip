@@ -19,7 +19,7 @@ thread_local std::string g_last_error;
 constexpr int kMaxDevices = 64;
 std::once_flag g_props_once[kMaxDevices];
 int g_is_gfx950[kMaxDevices];
-std::string g_arch[kMaxDevices];
+char g_arch[kMaxDevices][64];
 
 }  // namespace
 
@@ -117,6 +117,46 @@ int prepare(const kvssd_decode_desc* desc, const int32_t* table, void* workspace
   return plan_checked(desc, *units, workspace, workspace_bytes, kernel, splits);
 }
 
+// Both decode entry points: the split kernel, then (with `out`) the merge.
+int decode_call(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
+                const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens,
+                const int32_t* block_table, void* workspace, size_t workspace_bytes, float* out, float* lse,
+                void* stream) {
+  int units = 0, kernel = 0, splits = 0;
+  if (int rc = prepare(desc, block_table, workspace, workspace_bytes, &units, &kernel, &splits)) return rc;
+  if (!query || !packed_k || !packed_v || !scales_k || !scales_v || !valid_tokens)
+    return arg_error("a required buffer pointer is NULL");
+  DecodeArgs a{};
+  a.desc = *desc;
+  a.query = query;
+  a.packed_k = packed_k;
+  a.packed_v = packed_v;
+  a.scales_k = scales_k;
+  a.scales_v = scales_v;
+  a.valid = valid_tokens;
+  a.table = block_table;
+  a.units = units;
+  a.stream = static_cast<hipStream_t>(stream);
+  SplitPartials parts = carve_partials(workspace, splits, desc->query_heads, desc->head_dim);
+  const SplitPlan plan = plan_splits(*desc, units);
+  if (kernel == KVSSD_KERNEL_STAGED && !staged_aligned(a)) {
+    if (desc->kernel == KVSSD_KERNEL_STAGED)
+      return arg_error("staged matrix-core kernel needs 16-byte aligned packed arrays and scales");
+    kernel = KVSSD_KERNEL_MFMA;
+  }
+  if (kernel == KVSSD_KERNEL_MFMA && !mfma_aligned(a)) {
+    if (desc->kernel == KVSSD_KERNEL_MFMA)
+      return arg_error(
+          "matrix-core kernel needs 16-byte aligned packed arrays (8-byte for INT2) and 8-byte aligned scales");
+    kernel = KVSSD_KERNEL_GENERAL;
+  }
+  int rc = kernel == KVSSD_KERNEL_STAGED ? launch_staged(a, plan, parts)
+           : kernel == KVSSD_KERNEL_MFMA ? launch_mfma(a, plan, parts)
+                                         : launch_general(a, plan, parts);
+  if (rc != 0 || out == nullptr) return rc;
+  return launch_merge_splits(parts, splits, desc->query_heads, desc->head_dim, out, lse, a.stream);
+}
+
 }  // namespace
 }  // namespace kvssd
 
@@ -147,15 +187,15 @@ __attribute__((visibility("default"))) int kvssd_hip_device_ok(int device, char*
   std::call_once(g_props_once[device], [device] {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) == hipSuccess) {
-      g_arch[device] = prop.gcnArchName;
+      std::snprintf(g_arch[device], sizeof(g_arch[device]), "%s", prop.gcnArchName);
       g_is_gfx950[device] = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0;
     } else {
-      g_arch[device] = "unknown";
+      std::snprintf(g_arch[device], sizeof(g_arch[device]), "%s", "unknown");
       g_is_gfx950[device] = 0;
     }
   });
   if (!g_is_gfx950[device]) {
-    say("libkvssd_hip is built for gfx950 (MI355X); device " + std::to_string(device) + " is " + g_arch[device]);
+    say("libkvssd_hip is built for gfx950 (MI355X); device " + std::to_string(device) + " is " + std::string(g_arch[device]));
     return 0;
   }
   say("gfx950 HIP kernels available");
@@ -185,35 +225,8 @@ __attribute__((visibility("default"))) int kvssd_hip_decode_partials(
     const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
     const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens, const int32_t* block_table,
     void* workspace, size_t workspace_bytes, void* stream) {
-  int units = 0, kernel = 0, splits = 0;
-  if (int rc = prepare(desc, block_table, workspace, workspace_bytes, &units, &kernel, &splits)) return rc;
-  if (!query || !packed_k || !packed_v || !scales_k || !scales_v || !valid_tokens)
-    return arg_error("a required buffer pointer is NULL");
-  DecodeArgs a{};
-  a.desc = *desc;
-  a.query = query;
-  a.packed_k = packed_k;
-  a.packed_v = packed_v;
-  a.scales_k = scales_k;
-  a.scales_v = scales_v;
-  a.valid = valid_tokens;
-  a.table = block_table;
-  a.units = units;
-  a.stream = static_cast<hipStream_t>(stream);
-  SplitPartials parts = carve_partials(workspace, splits, desc->query_heads, desc->head_dim);
-  const SplitPlan plan = plan_splits(*desc, units);
-  if (kernel == KVSSD_KERNEL_STAGED) {
-    if (staged_aligned(a)) return launch_staged(a, plan, parts);
-    if (desc->kernel == KVSSD_KERNEL_STAGED)
-      return arg_error("staged matrix-core kernel needs 16-byte aligned packed arrays and scales");
-    kernel = KVSSD_KERNEL_MFMA;
-  }
-  if (kernel == KVSSD_KERNEL_MFMA) {
-    if (mfma_aligned(a)) return launch_mfma(a, plan, parts);
-    if (desc->kernel == KVSSD_KERNEL_MFMA)
-      return arg_error("matrix-core kernel needs 16-byte aligned packed arrays (8-byte for INT2) and 8-byte aligned scales");
-  }
-  return launch_general(a, plan, parts);
+  return decode_call(desc, query, packed_k, packed_v, scales_k, scales_v, valid_tokens, block_table, workspace,
+                     workspace_bytes, nullptr, nullptr, stream);
 }
 
 __attribute__((visibility("default"))) int kvssd_hip_decode_merge(const kvssd_decode_desc* desc,
@@ -234,10 +247,8 @@ __attribute__((visibility("default"))) int kvssd_hip_fused_decode(
     const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens, const int32_t* block_table,
     float* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   if (!out || !lse) return arg_error("a required buffer pointer is NULL");
-  if (int rc = kvssd_hip_decode_partials(desc, query, packed_k, packed_v, scales_k, scales_v, valid_tokens,
-                                         block_table, workspace, workspace_bytes, stream))
-    return rc;
-  return kvssd_hip_decode_merge(desc, workspace, workspace_bytes, out, lse, stream);
+  return decode_call(desc, query, packed_k, packed_v, scales_k, scales_v, valid_tokens, block_table, workspace,
+                     workspace_bytes, out, lse, stream);
 }
 
 __attribute__((visibility("default"))) int kvssd_hip_merge_chunks(int rows, int dim, float* acc_out, float* acc_lse,

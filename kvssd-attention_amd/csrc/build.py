@@ -21,6 +21,7 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 PKG = HERE.parent / "kvssd"
 OUT = PKG / "libkvssd_hip.so"
+TIMELINE_OUT = PKG / "libkvssd_hip_timeline.so"
 BUILD = HERE / "_build"
 SOURCES = ["abi.hip", "decode_general.hip", "decode_mfma.hip", "decode_staged.hip", "merge.hip", "codec.hip", "records.hip", "vllm_codec.hip"]
 ARCH = "gfx950"
@@ -61,27 +62,34 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
-def build(jobs: int = 0, verbose: bool = False) -> Path:
-    BUILD.mkdir(exist_ok=True)
+def build(jobs: int = 0, verbose: bool = False, timeline: bool = False) -> Path:
+    """Compile every source and link the library.  ``timeline`` builds the
+    instrumented variant (per-workgroup phase stamps, csrc/timeline.hpp) to
+    kvssd/libkvssd_hip_timeline.so instead; the product never loads it."""
+    out = TIMELINE_OUT if timeline else OUT
+    build_dir = BUILD / "timeline" if timeline else BUILD
+    build_dir.mkdir(parents=True, exist_ok=True)
     cc = hipcc()
-    objs = [BUILD / (Path(s).stem + ".o") for s in SOURCES]
-    cmds = [[cc, *COMMON, "-c", str(HERE / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
+    flags = [*COMMON, "-DKVSSD_TIMELINE"] if timeline else COMMON
+    objs = [build_dir / (Path(s).stem + ".o") for s in SOURCES]
+    cmds = [[cc, *flags, "-c", str(HERE / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
     workers = jobs or min(len(cmds), os.cpu_count() or 1)
     with ThreadPoolExecutor(max_workers=workers) as pool:
         for fut in [pool.submit(_run, c, verbose) for c in cmds]:
             fut.result()
-    tmp = OUT.with_suffix(".so.tmp")
+    tmp = out.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
-    os.replace(tmp, OUT)
-    return OUT
+    os.replace(tmp, out)
+    return out
 
 
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=0)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--timeline", action="store_true", help="build the instrumented library (phase stamps)")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose))
+    print(build(args.jobs, args.verbose, args.timeline))
 
 
 if __name__ == "__main__":

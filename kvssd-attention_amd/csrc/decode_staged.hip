@@ -56,6 +56,11 @@
 //   lane li -> token 16*tau + li.  W of QK lane li, tile tau lives in slot
 //   4*u + tau of its (h, g) row, u = 8((li>>1)&1) + 2(li>>2) + (li&1).
 #include "staged_ops.hpp"
+#include "timeline.hpp"
+
+#ifdef KVSSD_TIMELINE
+__device__ uint64_t kvssd_timeline_stamps[kvssd::kTimelineWgs * kvssd::kTimelineSlots];
+#endif
 
 namespace kvssd {
 namespace {
@@ -385,6 +390,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   constexpr int kWBytes = G::W_IN_K ? 0 : kWaves * QUADS * 2048;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * G::STAGE + kWBytes + kMaxUnits * 8];
 
+  KVSSD_STAMP(kStampEntry);
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int w = wave & (KG - 1);
@@ -454,11 +460,13 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
       issue_stage<BITS, KG>(p, lds0, Cursor{0, u_begin, 0, 0}, kvh0, wave, cm);
       spec = true;
     }
+    KVSSD_STAMP(kStampStage0Issued);
     // the query rows and the valid counts (issued first) have landed once at
     // most the stage's copies are outstanding (copies complete in issue order)
     if (spec) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies));
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
+    KVSSD_STAMP(kStampRowsLanded);
     coop_query_build<BITS, QUADS, QSPLIT>(qo, coop_query_load<BITS, QUADS, QT>(qrows, p.gq, w * p.gq, lane),
                                           p.scale_log2, lane, lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
     __syncthreads();  // query rows and scratch consumed: the second buffer is free
@@ -474,10 +482,12 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
       }
       if (issued1) issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>(G::STAGE), c1, kvh0, wave, cm);
     }
+    KVSSD_STAMP(kStampStage1Issued);
     // stage 0 and the valid counts landed (stage 1 may still be in flight)
     if (issued1) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies));
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
+    KVSSD_STAMP(kStampStage0Landed);
     have = advance(cur);
     wait0 = false;
     if (have && !(spec && cur.u == 0 && cur.sb0 == 0)) {
@@ -551,11 +561,14 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // copies go out right after the barrier
   int buf = 0;
   bool first = true;
+  int stage_no = 0;
+  KVSSD_STAMP(kStampLoop);
   while (have) {
     if (!first || wait0) {
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
       __syncthreads();                     // ... everyone's; and the other buffer is free
     }
+    KVSSD_STAMP(kStampStage + min(stage_no++, 15));
     if (have_n && !(first && pre1))
       issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>((buf ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
     first = false;
@@ -571,6 +584,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     buf ^= 1;
   }
 
+  KVSSD_STAMP(kStampLoopEnd);
   // -------------------------------------------------------------- epilogue
   // out = F (C - corr) per column: F = 64 (INT2 parity 0: 4, parity 1: 16)
   // lane (li, lq): column (head li/4, group li%4), rows = dims of its tiles
@@ -665,6 +679,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
       }
     }
   }
+  KVSSD_STAMP(kStampStored);
 }
 
 template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
@@ -759,3 +774,17 @@ int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials part
 }
 
 }  // namespace kvssd
+
+#ifdef KVSSD_TIMELINE
+// Instrumented build only (no declaration in include/kvssd_hip.h): copy the
+// stamps out, or clear them before a run.
+extern "C" __attribute__((visibility("default"))) int kvssd_hip_timeline_read(void* dst, size_t bytes) {
+  return static_cast<int>(hipMemcpyFromSymbol(dst, HIP_SYMBOL(kvssd_timeline_stamps), bytes, 0, hipMemcpyDeviceToHost));
+}
+extern "C" __attribute__((visibility("default"))) int kvssd_hip_timeline_clear(void) {
+  void* ptr = nullptr;
+  hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(kvssd_timeline_stamps));
+  if (err == hipSuccess) err = hipMemset(ptr, 0, sizeof(kvssd_timeline_stamps));
+  return static_cast<int>(err);
+}
+#endif

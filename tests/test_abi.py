@@ -143,3 +143,4 @@ def test_a_second_build_is_refused_in_the_same_process(tmp_path):
     with pytest.raises(RuntimeError, match="one process holds one build"):
         _native.load(other)
     assert _native.load() is lib
+
