@@ -106,6 +106,19 @@ int kvssd_hip_fused_decode(const kvssd_decode_desc* desc, const void* query, con
                            const int32_t* valid_tokens, const int32_t* block_table, float* out, float* lse,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* kvssd_hip_fused_decode with no workspace argument and no allocation: the
+ * split partials go to a 16 MiB array of device memory the library holds per
+ * GPU for the life of the process.  No counterpart in the reference; it is
+ * for callers that cannot allocate device memory (HIP graph capture, serving
+ * loops that forbid it).  Shapes whose partials need more than 16 MiB (see
+ * kvssd_hip_decode_workspace_bytes) fail with an argument error.  Calls that
+ * overlap on one GPU share the array and race: issue them on one stream (or
+ * order them) per GPU. */
+int kvssd_hip_fused_decode_static(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k,
+                                  const uint8_t* packed_v, const uint16_t* scales_k, const uint16_t* scales_v,
+                                  const int32_t* valid_tokens, const int32_t* block_table, float* out, float* lse,
+                                  void* stream);
+
 /* Phase 1 of kvssd_hip_fused_decode alone: every split writes its
  * unnormalised partial (O, running max, running sum) into `workspace`.
  * kvssd_hip_decode_merge turns them into (out, lse).  Same arguments and checks

@@ -117,6 +117,37 @@ int prepare(const kvssd_decode_desc* desc, const int32_t* table, void* workspace
   return plan_checked(desc, *units, workspace, workspace_bytes, kernel, splits);
 }
 
+// ------------------------------------------------ no-allocation decode ---
+// Split partials of kvssd_hip_fused_decode_static live in this file-scope
+// device array instead of a caller's workspace.  Each GPU the library runs on
+// holds its own copy (at its own address) until the process ends.  Host code
+// never passes the array's name to a kernel or a copy: `scratch` is a
+// host-side stand-in there; the device address comes from
+// hipGetSymbolAddress, once per device with that device current.  Nothing in
+// it has to start at zero: every split writes its whole partial before the
+// merge reads it.  Calls that overlap on one GPU share the array and race.
+constexpr size_t kStaticScratchBytes = size_t{16} << 20;  // 16 MiB
+static __device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+int static_scratch(void** ptr) {
+  int dev = 0;
+  if (hipError_t err = hipGetDevice(&dev); err != hipSuccess) return hip_status(err, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return arg_error("HIP device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); err != hipSuccess)
+      return hip_status(err, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return hip_status(hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return 0;
+}
+
 // Both decode entry points: the split kernel, then (with `out`) the merge.
 int decode_call(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
                 const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens,
@@ -249,6 +280,23 @@ __attribute__((visibility("default"))) int kvssd_hip_fused_decode(
   if (!out || !lse) return arg_error("a required buffer pointer is NULL");
   return decode_call(desc, query, packed_k, packed_v, scales_k, scales_v, valid_tokens, block_table, workspace,
                      workspace_bytes, out, lse, stream);
+}
+
+__attribute__((visibility("default"))) int kvssd_hip_fused_decode_static(
+    const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
+    const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens, const int32_t* block_table,
+    float* out, float* lse, void* stream) {
+  if (!out || !lse) return arg_error("a required buffer pointer is NULL");
+  size_t need = 0;
+  if (int rc = kvssd_hip_decode_workspace_bytes(desc, &need)) return rc;
+  if (need > kStaticScratchBytes)
+    return arg_error("this shape needs " + std::to_string(need) + " bytes of split partials, more than the " +
+                     std::to_string(kStaticScratchBytes) +
+                     "-byte static scratch; use kvssd_hip_fused_decode with a workspace");
+  void* ptr = nullptr;
+  if (int rc = static_scratch(&ptr)) return rc;
+  return decode_call(desc, query, packed_k, packed_v, scales_k, scales_v, valid_tokens, block_table, ptr,
+                     kStaticScratchBytes, out, lse, stream);
 }
 
 __attribute__((visibility("default"))) int kvssd_hip_merge_chunks(int rows, int dim, float* acc_out, float* acc_lse,

@@ -68,6 +68,7 @@ SIGNATURES = {
     "kvssd_hip_decode_workspace_bytes": (_I, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(_SZ)]),
     "kvssd_hip_decode_kernel": (_I, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(_I)]),
     "kvssd_hip_fused_decode": (_I, [ctypes.POINTER(DecodeDesc)] + [_VP] * 10 + [_SZ, _VP]),
+    "kvssd_hip_fused_decode_static": (_I, [ctypes.POINTER(DecodeDesc)] + [_VP] * 10),
     "kvssd_hip_decode_partials": (_I, [ctypes.POINTER(DecodeDesc)] + [_VP] * 8 + [_SZ, _VP]),
     "kvssd_hip_decode_merge": (_I, [ctypes.POINTER(DecodeDesc), _VP, _SZ, _VP, _VP, _VP]),
     "kvssd_hip_merge_chunks": (_I, [_I, _I, _VP, _VP, _VP, _VP, _VP]),

@@ -144,3 +144,17 @@ def test_a_second_build_is_refused_in_the_same_process(tmp_path):
         _native.load(other)
     assert _native.load() is lib
 
+
+def test_static_scratch_decode_rejects_shapes_beyond_its_limit():
+    # 64 query heads over one kv head, head_dim 256, 4096 blocks: 1024 splits of
+    # 64 x 258 floats = 67 MB of partials, more than the 16 MiB scratch; the
+    # call fails before any device work
+    lib = _native.load()
+    desc = _native.DecodeDesc(64, 1, 256, 4096, 16, 4, 32, 2, 0, 0, 0.1)
+    n = ctypes.c_size_t(0)
+    assert lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(n)) == 0 and n.value > 16 << 20
+    fake = [ctypes.c_void_p(256)] * 6
+    rc = lib.kvssd_hip_fused_decode_static(ctypes.byref(desc), *fake, None, ctypes.c_void_p(256), ctypes.c_void_p(256),
+                                           None)
+    assert rc < 0 and "static scratch" in _native.last_error()
+    assert lib.kvssd_hip_fused_decode_static(ctypes.byref(desc), *fake, None, None, None, None) < 0
