@@ -19,7 +19,7 @@ the pipeline's page-locked staging ring is what crosses PCIe.
 from __future__ import annotations
 
 from collections import deque
-from collections.abc import Sequence
+from collections.abc import Callable, Sequence
 from concurrent.futures import Future, ThreadPoolExecutor
 from dataclasses import dataclass
 from queue import Queue
@@ -101,6 +101,13 @@ class AsyncBlockLoader:
         """Raw records of ``block_ids`` into rows 0..n-1 of ``destination``
         (a contiguous CPU uint8 tensor [>= n, record_bytes]), read on the I/O
         threads.  No header or CRC check happens here."""
+        self.read_records_async(layer, block_ids, destination)()
+
+    def read_records_async(
+        self, layer: int, block_ids: Sequence[int], destination: torch.Tensor
+    ) -> Callable[[], None]:
+        """As read_records, returning as soon as the reads are queued; the
+        returned callable waits for all of them and raises the first error."""
         rb = self.store.spec.record_bytes
         if (
             destination.device.type != "cpu"
@@ -128,12 +135,16 @@ class AsyncBlockLoader:
                 self.free.put(slot)
 
         futures = [self.executor.submit(work, e, destination[i]) for i, e in enumerate(entries)]
-        # every read finishes before the first error is raised, so no worker
-        # still writes into the destination afterwards
-        errors = [f.exception() for f in futures]
-        for err in errors:
-            if err is not None:
-                raise err
+
+        def wait() -> None:
+            # every read finishes before the first error is raised, so no
+            # worker still writes into the destination afterwards
+            errors = [f.exception() for f in futures]
+            for err in errors:
+                if err is not None:
+                    raise err
+
+        return wait
 
     def close(self) -> None:
         self.executor.shutdown(wait=True, cancel_futures=False)

@@ -61,6 +61,7 @@ class KVSSDPipeline:
         stage_blocks: int = 4,
         require_cuda_kernel: bool = False,
         attention_backend: str | AttentionBackend | None = None,
+        defer_record_checks: bool = False,
     ):
         self.store = store
         self.device = torch.device(device)
@@ -77,6 +78,11 @@ class KVSSDPipeline:
         # a second copy stream: successive chunks alternate between the two
         self._transfer_alt = torch.cuda.Stream(device=self.device) if gpu else None
         self.compute_stream = torch.cuda.Stream(device=self.device) if gpu else None
+        # streamed decodes check their records' CRC and headers before
+        # returning (the reference's behaviour); deferred, a decode returns
+        # without waiting for the GPU and a bad record raises at the next
+        # streamed decode, synchronize() or close()
+        self.defer_record_checks = defer_record_checks
         self._stager: RecordStager | None = None
         self._resident: dict[int, _Resident] = {}
         self._host: dict[int, HostRecords] = {}
@@ -97,6 +103,7 @@ class KVSSDPipeline:
                 [self.transfer_stream, self._transfer_alt],
                 self.compute_stream,
             )
+            self._stager.defer_checks = self.defer_record_checks
         return self._stager
 
     def _read_layer(self, layer: int) -> HostRecords:
@@ -114,7 +121,7 @@ class KVSSDPipeline:
         if host is not None:
             fill = stager.host_fill(host)
         else:
-            fill = stager.read_fill(lambda ids, rows: self.loader.read_records(layer, ids, rows))
+            fill = stager.read_fill(lambda ids, rows: self.loader.read_records_async(layer, ids, rows))
         out, _ = stager.run(query, 1.0 / math.sqrt(query.shape[-1]), layer, selected, fill)
         return out.to(query.dtype)
 
@@ -203,10 +210,21 @@ class KVSSDPipeline:
             attention_backend=self.attention_backend,
         )
 
+    def synchronize(self) -> None:
+        """Wait for the pipeline's GPU work; raise for any deferred record error."""
+        if self._stager is not None:
+            self._stager.check_pending()
+        if self.device.type == "cuda":
+            torch.cuda.synchronize(self.device)
+
     def close(self) -> None:
-        self.loader.close()
-        self._resident.clear()
-        self._host.clear()
+        try:
+            if self._stager is not None:
+                self._stager.check_pending()
+        finally:
+            self.loader.close()
+            self._resident.clear()
+            self._host.clear()
 
     def __enter__(self) -> "KVSSDPipeline":
         return self

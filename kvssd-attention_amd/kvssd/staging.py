@@ -150,6 +150,52 @@ class HostRecords:
 Fill = Callable[[Sequence[int], Slot], list[Span]]
 
 
+class ReadFill:
+    """Chunks read from storage into a slot's page-locked host memory, one
+    chunk ahead of the one being staged: ``prefetch`` queues the reads of a
+    later chunk (once the slot's previous copy out of that memory is done) and
+    the fill of that chunk waits for them, so the loader's threads read chunk
+    i + 2 while chunk i + 1 crosses PCIe and chunk i is decoded."""
+
+    def __init__(self, record_bytes: int, read: Callable[[Sequence[int], torch.Tensor], Callable[[], None]]):
+        self.record_bytes = record_bytes
+        self.read = read
+        self.pending: dict[int, tuple[tuple[int, ...], Callable[[], None]]] = {}
+
+    def prefetch(self, ids: Sequence[int], slot: Slot) -> None:
+        self.drain(slot)
+        slot.host_ready()
+        self.pending[id(slot)] = (tuple(ids), self.read(ids, slot.host))
+
+    def drain(self, slot: Slot) -> None:
+        got = self.pending.pop(id(slot), None)
+        if got is not None:
+            got[1]()
+
+    def drain_all(self) -> None:
+        """Wait for every queued read (a run that stops early leaves none behind)."""
+        pending, self.pending = self.pending, {}
+        errors = []
+        for _, wait in pending.values():
+            try:
+                wait()
+            except Exception as exc:  # reported only if nothing else was raised
+                errors.append(exc)
+        if errors:
+            raise errors[0]
+
+    def __call__(self, ids: Sequence[int], slot: Slot) -> list[Span]:
+        got = self.pending.pop(id(slot), None)
+        if got is not None and got[0] == tuple(ids):
+            got[1]()
+        else:
+            if got is not None:
+                got[1]()
+            slot.host_ready()
+            self.read(ids, slot.host)()
+        return [(slot.host.data_ptr(), 0, len(ids) * self.record_bytes)]
+
+
 class RecordStager:
     """Staging ring plus chunk loop: ``run`` attends over the records of
     ``block_ids`` in chunks of ``stage_blocks`` and returns (out f32, lse f32)."""
@@ -184,6 +230,9 @@ class RecordStager:
             spec.bits, spec.block_tokens, spec.kv_heads, spec.head_dim, spec.group_size
         )
         self.last_enqueue_seconds = 0.0  # host time the last run spent issuing its chunks
+        # record statuses of a run whose check is deferred: (event, host codes, layer, ids)
+        self.defer_checks = False
+        self._pending: tuple[torch.cuda.Event, torch.Tensor, int, list[int]] | None = None
 
     # ------------------------------------------------------------- fills ---
     def host_fill(self, host: HostRecords) -> Fill:
@@ -191,16 +240,10 @@ class RecordStager:
         rb = self.spec.record_bytes
         return lambda ids, slot: host.spans(ids, rb)
 
-    def read_fill(self, read: Callable[[Sequence[int], torch.Tensor], None]) -> Fill:
-        """Chunks read by ``read(ids, rows)`` into the slot's host memory."""
-        rb = self.spec.record_bytes
-
-        def fill(ids: Sequence[int], slot: Slot) -> list[Span]:
-            slot.host_ready()
-            read(ids, slot.host)
-            return [(slot.host.data_ptr(), 0, len(ids) * rb)]
-
-        return fill
+    def read_fill(self, read: Callable[[Sequence[int], torch.Tensor], Callable[[], None]]) -> "ReadFill":
+        """Chunks read into the slot's host memory by ``read(ids, rows)``,
+        which queues the reads and returns their waiter."""
+        return ReadFill(self.spec.record_bytes, read)
 
     # -------------------------------------------------------------- loop ---
     def _stage(self, index: int, ids: Sequence[int], fill: Fill) -> None:
@@ -218,6 +261,12 @@ class RecordStager:
             _native.check(rc, "kvssd_hip_memcpy_h2d_async")
         slot.copied_event().record(transfer)
 
+    def _prefetch(self, index: int, chunks: list[list[int]], fill: Fill) -> None:
+        """Queue the reads of chunk ``index`` into its slot, if the fill reads."""
+        prefetch = getattr(fill, "prefetch", None)
+        if prefetch is not None and index < len(chunks):
+            prefetch(chunks[index], self.slots[index % len(self.slots)])
+
     def _merge(self, acc, out: torch.Tensor, lse: torch.Tensor):
         if acc is None:
             return out, lse
@@ -227,9 +276,22 @@ class RecordStager:
             return acc
         return merge_attention_chunks(acc[0], acc[1], out, lse)
 
+    def check_pending(self) -> None:
+        """Raise for the records of a deferred run (blocks until it finished)."""
+        pending, self._pending = self._pending, None
+        if pending is not None:
+            event, codes, layer, ids = pending
+            event.synchronize()
+            raise_for_status(codes, layer, ids)
+
     def run(
         self, query: torch.Tensor, sm_scale: float, layer: int, block_ids: Sequence[int], fill: Fill
     ) -> tuple[torch.Tensor, torch.Tensor]:
+        """Attention over the records of ``block_ids``.  Their statuses are
+        checked before the call returns (the reference's behaviour), or, with
+        ``defer_checks``, at the start of the next run or in check_pending, so
+        that a loop over layers never waits for the GPU."""
+        self.check_pending()
         chunks = [list(block_ids[i : i + self.stage_blocks]) for i in range(0, len(block_ids), self.stage_blocks)]
         if not chunks:
             raise ValueError("selector returned no blocks")
@@ -240,13 +302,23 @@ class RecordStager:
         with torch.cuda.stream(compute):
             status = torch.empty(len(block_ids), dtype=torch.int32, device=self.device)
             t0 = time.perf_counter()
-            if isinstance(self.backend, HipAttentionBackend) and query.dtype in _native.QUERY_DTYPES:
-                acc = self._loop_native(query, sm_scale, chunks, fill, status)
-            else:
-                acc = self._loop_generic(query, sm_scale, chunks, fill, status)
+            try:
+                if isinstance(self.backend, HipAttentionBackend) and query.dtype in _native.QUERY_DTYPES:
+                    acc = self._loop_native(query, sm_scale, chunks, fill, status)
+                else:
+                    acc = self._loop_generic(query, sm_scale, chunks, fill, status)
+            finally:
+                drain_all = getattr(fill, "drain_all", None)
+                if drain_all is not None:
+                    drain_all()
             self.last_enqueue_seconds = time.perf_counter() - t0
-            codes = status.cpu()  # waits for the compute stream
-        raise_for_status(codes, layer, list(block_ids))
+            codes = torch.empty(status.shape, dtype=status.dtype, pin_memory=True)
+            codes.copy_(status, non_blocking=True)
+            ready = torch.cuda.Event()
+            ready.record(compute)
+        self._pending = (ready, codes, layer, list(block_ids))
+        if not self.defer_checks:
+            self.check_pending()
         done = torch.cuda.Event()
         done.record(compute)
         caller.wait_event(done)
@@ -259,6 +331,7 @@ class RecordStager:
         spec, sb, compute = self.spec, self.stage_blocks, self.compute_stream
         acc = None
         self._stage(0, chunks[0], fill)
+        self._prefetch(1, chunks, fill)
         for i, ids in enumerate(chunks):
             slot = self.slots[i % len(self.slots)]
             n = len(ids)
@@ -271,6 +344,7 @@ class RecordStager:
             slot.consumed_event().record(compute)
             if i + 1 < len(chunks):
                 self._stage(i + 1, chunks[i + 1], fill)
+                self._prefetch(i + 2, chunks, fill)
         assert acc is not None
         return acc
 
@@ -315,6 +389,7 @@ class RecordStager:
         qp, wp = q.data_ptr(), work.data_ptr()
         sp = status.data_ptr()
         self._stage(0, chunks[0], fill)
+        self._prefetch(1, chunks, fill)
         for i, ids in enumerate(chunks):
             slot = self.slots[i % len(self.slots)]
             n = len(ids)
@@ -337,4 +412,5 @@ class RecordStager:
             slot.consumed_event().record(compute)
             if i + 1 < len(chunks):
                 self._stage(i + 1, chunks[i + 1], fill)
+                self._prefetch(i + 2, chunks, fill)
         return acc_out, acc_lse
