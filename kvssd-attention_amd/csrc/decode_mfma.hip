@@ -44,9 +44,12 @@
 //           R*32 + 8*(n ^ 2*(T&1)).
 //   W: [quad][h*4+g][slot], rows of 272 B (256 B + 16 B pad), slot for token
 //      16*tau + t at 32*(t%4) + 8*(t/4) + dimperm^-1(tau).
-// Non-fp16 queries are normalised per head by a power of two and split into
-// hi + lo fp16 parts (two MFMAs per step); the power of two returns in the
-// score scale, so the products stay exact.
+// Non-fp16 queries are normalised per head by a power of two, fp32 and fp64
+// ones split into hi + lo fp16 parts (two MFMAs per step; bf16 values fit one
+// part); the power of two returns in the score scale, so the products stay
+// exact.
+#include <type_traits>
+
 #include "decode.hpp"
 
 namespace kvssd {
@@ -377,6 +380,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
   if (have0) issue_loads<BITS>(s0, p, c0, kvh, li, lq);
 
   // ---------------------------------------------------------------- query
+  constexpr bool kNormalise = !std::is_same<QT, _Float16>::value;
   u32x4 qa[QUADS][QSPLIT][4];
   f32x4 qcorr[QUADS];
   float kscale[QUADS];
@@ -386,7 +390,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
     const int hrow = quad * 4 + lq;  // head of this lane's QK row
     const int hrow_c = hrow < p.gq ? hrow : p.gq - 1;
     float e_row = 0.0f;
-    if (QSPLIT == 2) {
+    if (kNormalise) {
       float mx = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(query_at<QT>(p, head0 + hrow_c, 8 * li + i)));
@@ -411,7 +415,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
       for (int s = 0; s < 8; ++s) {
         const float raw = query_at<QT>(p, head0 + ha_c, qk_dim<BITS>(m, lq, s));
         float x = live ? raw : 0.0f;
-        if (QSPLIT == 2) x = ldexpf(x, -static_cast<int>(e_a));
+        if (kNormalise) x = ldexpf(x, -static_cast<int>(e_a));
         hi[s] = static_cast<_Float16>(x);
         lo[s] = static_cast<_Float16>(x - static_cast<float>(hi[s]));
       }
@@ -427,7 +431,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       float x = query_at<QT>(p, head0 + hrow_c, 8 * li + i);
-      if (QSPLIT == 2) x = ldexpf(x, -static_cast<int>(e_row));
+      if (kNormalise) x = ldexpf(x, -static_cast<int>(e_row));
       const _Float16 h16 = static_cast<_Float16>(x);
       const float rep = QSPLIT == 2 ? static_cast<float>(h16) +
                                           static_cast<float>(static_cast<_Float16>(x - static_cast<float>(h16)))
@@ -527,8 +531,8 @@ int launch_quads(const MfmaParams& prm, int grid, int dtype, hipStream_t s) {
     case KVSSD_DTYPE_F16:
       launch_one<BITS, QUADS, 1, _Float16>(prm, grid, s);
       break;
-    case KVSSD_DTYPE_BF16:
-      launch_one<BITS, QUADS, 2, uint16_t>(prm, grid, s);
+    case KVSSD_DTYPE_BF16:  // 8 significant bits: one fp16 part holds a normalised value exactly
+      launch_one<BITS, QUADS, 1, uint16_t>(prm, grid, s);
       break;
     case KVSSD_DTYPE_F32:
       launch_one<BITS, QUADS, 2, float>(prm, grid, s);

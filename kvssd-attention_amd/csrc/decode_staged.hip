@@ -34,9 +34,9 @@
 //
 // Code -> fp16 without a dequantised tensor: a code c in the mantissa of an
 // fp16 whose exponent is that of 1.0 reads as v = 1 + c/F, and
-// (c - mid) = F (v - OFF) with OFF = 1 + mid/F (F = 64 for INT4; 4 or 16 per
-// slot for INT2, absorbed by the query operand in QK and by the output factor
-// in PV).  The offset is removed through the accumulator: QK starts from
+// (c - mid) = F (v - OFF) with OFF = 1 + mid/F (F = 1024 or 64 per slot for
+// INT4, 64, 16 or 4 for INT2; absorbed by the query operand in QK and by W or
+// the output factor in PV).  The offset is removed through the accumulator: QK starts from
 // -sum q' OFF, PV subtracts an extra MFMA of W against OFF.
 //
 // QK (v_mfma_f32_16x16x32_f16): A = query, rows (h, g) = 4 heads x 4 groups,
@@ -46,11 +46,13 @@
 // softmax: per-stage max by 16-lane DPP reduction, running (m, l) in log2
 //   units, p = 2^(s - m).  W[t, (h, g)] = p * scale_v[t, g] in fp16,
 //   written to LDS.
-// PV (v_mfma_f32_16x16x32_f16): A = V^T codes from a 16x16 nibble transpose
-//   read (ds_read_b64_tr_b4) of the staged V rows: one transpose read covers
-//   all 64 tokens of a wave's half for 16 dims (INT4) / 32 dims (INT2).
-//   B = W, columns (h, g); only the column whose group owns a tile's dims is
-//   kept.
+// PV (v_mfma_f32_16x16x32_f16): A = W^T, rows (h, g); B = V codes from a
+//   16x16 nibble transpose read (ds_read_b64_tr_b4) of the staged V rows, one
+//   column per dim: one transpose read covers all 64 tokens of a wave's half
+//   for 16 dims (INT4) / 32 dims (INT2).  Lane (li, lq) ends with rows
+//   (head lq, groups 0..3) of its dim, of which it keeps the group that owns
+//   the dim -- the same head as its scores, so the softmax rescale needs no
+//   exchange between lanes and touches only the kept entries.
 // Token <-> MFMA K slot (PV, shared by A and B): K step kk, lane group q,
 //   slot s -> token 16*(s&3) + 4q + 2kk + (s>>2) of the half; QK tile tau,
 //   lane li -> token 16*tau + li.  W of QK lane li, tile tau lives in slot
@@ -127,10 +129,17 @@ __device__ __forceinline__ int chunk_byte(int t, int idx) {
 }
 
 // Per-lane byte offsets (relative to the stage's group base) of this wave's
-// copy instructions: code regions (same map for K and V) and one scale copy.
+// copy instructions.  Copy j of a code region (lane positions 64 (wave + 8 j)
+// + lane) covers token row t0 + j * 512 / CPT, with copy 0's slot: its
+// swizzle differs from copy 0's by phi(j * 512 / CPT) whatever t0 (the row's
+// bits 4 and up reach phi only as an XOR of chunk bits, and t0's low bits are
+// the same for every j), so two registers serve every copy: the row offset
+// and the swizzled chunk offset, XORed with a constant per copy; the row step
+// goes into the scalar base.  One more register holds the scale copy's offset.
 template <int BITS, int KG>
 struct CopyMap {
-  uint32_t kv[Geo<BITS, KG>::KV_PER_WAVE];
+  uint32_t row;    // t0 * row stride
+  uint32_t chunk;  // 16 * (slot ^ phi(t0))
   uint32_t sc;
 };
 
@@ -138,13 +147,10 @@ template <int BITS, int KG>
 __device__ __forceinline__ CopyMap<BITS, KG> make_copy_map(int wave, int lane, int kv_heads) {
   using G = Geo<BITS, KG>;
   CopyMap<BITS, KG> cm;
-  const int rs = kv_heads * G::PD;
-#pragma unroll
-  for (int j = 0; j < G::KV_PER_WAVE; ++j) {
-    const int pos = 64 * (wave + kWaves * j) + lane;
-    const int t = pos / G::CPT, slot = pos % G::CPT;
-    cm.kv[j] = static_cast<uint32_t>(t * rs + 16 * (slot ^ phi<G::CPT>(t)));
-  }
+  const int pos0 = 64 * wave + lane;
+  const int t0 = pos0 / G::CPT, slot0 = pos0 % G::CPT;
+  cm.row = static_cast<uint32_t>(t0 * kv_heads * G::PD);
+  cm.chunk = static_cast<uint32_t>(16 * (slot0 ^ phi<G::CPT>(t0)));
   const int pos = 64 * (wave & 3) + lane;
   const int t = pos / G::SCPT, slot = pos % G::SCPT;
   cm.sc = static_cast<uint32_t>(t * kv_heads * 8 + 16 * (slot ^ phi<G::SCPT>(t)));
@@ -155,17 +161,21 @@ template <int BITS, int KG>
 __device__ __forceinline__ void issue_stage(const StagedParams& p, uint32_t buf, const Cursor& c, int kvh0, int wave,
                                             const CopyMap<BITS, KG>& cm) {
   using G = Geo<BITS, KG>;
+  constexpr int kRowStep = kThreads / G::CPT;  // token rows between a wave's copies
   const long row0 = (static_cast<long>(c.blk) * p.block_tokens + c.sb0) * p.kv_heads + kvh0;
-  const uint8_t* kb = p.pk + row0 * G::PD;
-  const uint8_t* vb = p.pv + row0 * G::PD;
+  // the scale copy first: should its offset ever be reloaded from scratch, the
+  // wait for it does not also wait for this stage's code copies
+  const uint8_t* sb = (wave < 4 ? p.sk : p.sv) + row0 * 8;
+  dma16<false>(sb, cm.sc, buf + (wave < 4 ? G::SK_OFF : G::SV_OFF) + 1024u * static_cast<uint32_t>(wave & 3));
+  const long rs = static_cast<long>(p.kv_heads) * G::PD;
 #pragma unroll
   for (int j = 0; j < G::KV_PER_WAVE; ++j) {
     const uint32_t i = static_cast<uint32_t>(wave + kWaves * j);
-    dma16<true>(kb, cm.kv[j], buf + G::K_OFF + 1024u * i);
-    dma16<true>(vb, cm.kv[j], buf + G::V_OFF + 1024u * i);
+    const uint32_t off = (cm.chunk ^ static_cast<uint32_t>(16 * phi<G::CPT>(j * kRowStep))) + cm.row;
+    const long step = static_cast<long>(j) * kRowStep * rs;
+    dma16<true>(p.pk + row0 * G::PD + step, off, buf + G::K_OFF + 1024u * i);
+    dma16<true>(p.pv + row0 * G::PD + step, off, buf + G::V_OFF + 1024u * i);
   }
-  const uint8_t* sb = (wave < 4 ? p.sk : p.sv) + row0 * 8;
-  dma16<false>(sb, cm.sc, buf + (wave < 4 ? G::SK_OFF : G::SV_OFF) + 1024u * static_cast<uint32_t>(wave & 3));
 }
 
 // W chunk (quad, row R = 4h + g, chunk c of 8 slots) byte offset.
@@ -280,7 +290,6 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
   float score[QUADS][4];
 #pragma unroll
   for (int tau = 0; tau < 4; ++tau) {
-    const bool ok = 16 * tau + li < hv;
 #pragma unroll
     for (int quad = 0; quad < QUADS; ++quad) {
       const f32x4 c = cc[quad][tau];
@@ -288,7 +297,19 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
       raw = __builtin_fmaf(half_hi(skw[tau][0]), c[1], raw);
       raw = __builtin_fmaf(half_lo(skw[tau][1]), c[2], raw);
       raw = __builtin_fmaf(half_hi(skw[tau][1]), c[3], raw);
-      score[quad][tau] = ok ? raw * qo.kscale[quad] : -INFINITY;
+      score[quad][tau] = raw * qo.kscale[quad];
+    }
+  }
+  // a partial stage (uniform branch): tokens past the valid count get score
+  // -inf and value scale 0 (p is 0 there, but the stale scale may not be finite)
+  if (hv < kHalfTok) {
+#pragma unroll
+    for (int tau = 0; tau < 4; ++tau) {
+      if (16 * tau + li >= hv) {
+#pragma unroll
+        for (int quad = 0; quad < QUADS; ++quad) score[quad][tau] = -INFINITY;
+        svw[tau] = u32x2{0u, 0u};
+      }
     }
   }
   // --------------------------------------------- V operands (no softmax dep)
@@ -318,21 +339,20 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
 #pragma unroll
     for (int tau = 0; tau < 4; ++tau) pr[tau] = __builtin_amdgcn_exp2f(score[quad][tau] - m_use);
     st.l_run[quad] = st.l_run[quad] * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-    // W = p * scale_v in fp16, masked tokens carry scale 0; INT4 tiles 0, 1
-    // sit in the K slots with F = 1024, so their W carries F/64 = 16
+    // W = p * scale_v in fp16 (masked tokens: p = 0, scale 0); INT4 tiles
+    // 0, 1 sit in the K slots with F = 1024, so their W carries F/64 = 16.
+    // Each fp16 pair is one mixed-precision FMA into each half.
     uint32_t wlo[4], whi[4];  // per group g: (tile 0, tile 1), (tile 2, tile 3)
 #pragma unroll
     for (int tau = 0; tau < 4; tau += 2) {
-      const bool ok0 = score[quad][tau] != -INFINITY;
-      const bool ok1 = score[quad][tau + 1] != -INFINITY;
       const float wfac = (BITS == 4 && tau == 0) ? 16.0f : 1.0f;
       const float p0 = pr[tau] * wfac, p1 = pr[tau + 1] * wfac;
-      const uint32_t a01 = ok0 ? svw[tau][0] : 0u, a23 = ok0 ? svw[tau][1] : 0u;
-      const uint32_t b01 = ok1 ? svw[tau + 1][0] : 0u, b23 = ok1 ? svw[tau + 1][1] : 0u;
-      const uint32_t w0 = pack_half2(static_cast<_Float16>(p0 * half_lo(a01)), static_cast<_Float16>(p1 * half_lo(b01)));
-      const uint32_t w1 = pack_half2(static_cast<_Float16>(p0 * half_hi(a01)), static_cast<_Float16>(p1 * half_hi(b01)));
-      const uint32_t w2 = pack_half2(static_cast<_Float16>(p0 * half_lo(a23)), static_cast<_Float16>(p1 * half_lo(b23)));
-      const uint32_t w3 = pack_half2(static_cast<_Float16>(p0 * half_hi(a23)), static_cast<_Float16>(p1 * half_hi(b23)));
+      const uint32_t a01 = svw[tau][0], a23 = svw[tau][1];
+      const uint32_t b01 = svw[tau + 1][0], b23 = svw[tau + 1][1];
+      const uint32_t w0 = wpair(p0, half_lo(a01), p1, half_lo(b01));
+      const uint32_t w1 = wpair(p0, half_hi(a01), p1, half_hi(b01));
+      const uint32_t w2 = wpair(p0, half_lo(a23), p1, half_lo(b23));
+      const uint32_t w3 = wpair(p0, half_hi(a23), p1, half_hi(b23));
       if (tau == 0) {
         wlo[0] = w0; wlo[1] = w1; wlo[2] = w2; wlo[3] = w3;
       } else {
@@ -344,15 +364,14 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
       const int off = w_chunk<BITS, QUADS, KG>(quad, 4 * lq + g, u >> 1, w, half) + 8 * (u & 1);
       *reinterpret_cast<u32x2*>(wbase + off) = u32x2{wlo[g], whi[g]};
     }
-    // rescale the PV state of column head li/4 by that head's alpha (alpha
-    // is uniform over each row: head h in lanes 16h .. 16h+15)
-    const RowValue a_pv = row_value(alpha, li >> 2);
-    if (a_pv.any_not_one) {
+    // rescale the PV state of head lq (the same head as this lane's scores):
+    // only the entries the epilogue reads, group k/2 of tile k
 #pragma unroll
-      for (int n = 0; n < 8; ++n) st.acc[quad][n] *= a_pv.v;
+    for (int k = 0; k < 8; ++k) st.acc[quad][k][k >> 1] *= alpha;
 #pragma unroll
-      for (int c = 0; c < NPAR; ++c) st.corr[quad][c] *= a_pv.v;
-    }
+    for (int c = 0; c < NPAR; ++c)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) st.corr[quad][c][g] *= alpha;
   }
   // -------------------------------------------------------------------- PV
   if constexpr (!kEarlyV) {
@@ -373,14 +392,14 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
       for (int par = 0; par < NPAR; ++par)
 #pragma unroll
         for (int quad = 0; quad < QUADS; ++quad)
-          st.acc[quad][NPAR * n + par] = mfma16(va[n][kk][par], wb[quad][kk], st.acc[quad][NPAR * n + par]);
-  // sum over tokens of W * OFF per column, through the matrix core
+          st.acc[quad][NPAR * n + par] = mfma16(wb[quad][kk], va[n][kk][par], st.acc[quad][NPAR * n + par]);
+  // sum over tokens of W * OFF per row, through the matrix core
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-      for (int c = 0; c < NPAR; ++c) st.corr[quad][c] = mfma16(offa[c], wb[quad][kk], st.corr[quad][c]);
+      for (int c = 0; c < NPAR; ++c) st.corr[quad][c] = mfma16(wb[quad][kk], offa[c], st.corr[quad][c]);
 }
 
 template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
@@ -541,8 +560,8 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   if (BITS == 4) {
     offa[0] = off_operand4();
   } else {
-    offa[0] = off_operand(1.5f);
-    offa[BITS == 4 ? 0 : 1] = off_operand(1.125f);
+    offa[0] = off_operand(1.5f);                 // parity 0: F = 4
+    offa[BITS == 4 ? 0 : 1] = off_operand(1.125f);  // parity 1: F = 16
   }
 
   WaveState<BITS, QUADS> st;
@@ -586,8 +605,10 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
 
   KVSSD_STAMP(kStampLoopEnd);
   // -------------------------------------------------------------- epilogue
-  // out = F (C - corr) per column: F = 64 (INT2 parity 0: 4, parity 1: 16)
-  // lane (li, lq): column (head li/4, group li%4), rows = dims of its tiles
+  // lane (li, lq) holds head lq of each quad; the entry of tile k it keeps
+  // is that of group k/2: dim 16k + li (INT4) or 32(k/2) + 2li + (k & 1)
+  // (INT2), and out = F (C - corr) with F = 64 (INT4) or 4 / 16 (INT2
+  // parity 0 / 1)
   float* xo = reinterpret_cast<float*>(lds);  // [w][quad][lane][8] from half 1
   float* xm = xo + KG * QUADS * 64 * 8;       // [w][quad][4 heads][2]
   __builtin_amdgcn_s_waitcnt(0x0F70);  // no copy of this wave is still writing LDS
@@ -596,38 +617,23 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   float mh[QUADS], lh[QUADS];
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
-    const int g = li & 3;
 #pragma unroll
-    for (int gg = 0; gg < 4; ++gg) {
-      if (gg == g) {
-        if (BITS == 4) {
-          const float cr = st.corr[quad][0][0];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            ov[quad][i] = 64.0f * (st.acc[quad][2 * gg][i] - cr);
-            ov[quad][4 + i] = 64.0f * (st.acc[quad][2 * gg + 1][i] - cr);
-          }
-        } else {
-          const float c0 = st.corr[quad][0][0], c1 = st.corr[quad][BITS == 4 ? 0 : 1][0];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            ov[quad][i] = 4.0f * (st.acc[quad][2 * gg][i] - c0);
-            ov[quad][4 + i] = 16.0f * (st.acc[quad][2 * gg + 1][i] - c1);
-          }
-        }
-      }
+    for (int k = 0; k < 8; ++k) {
+      const int g = k >> 1;
+      const int c = BITS == 4 ? 0 : (k & 1);
+      const float f = BITS == 4 ? 64.0f : ((k & 1) ? 16.0f : 4.0f);
+      ov[quad][k] = f * (st.acc[quad][k][g] - st.corr[quad][c][g]);
     }
-    // (m, l) of head li/4 (the QK layout keeps head lq in lanes 16lq..16lq+15)
-    const float l_tot = row_sum16(st.l_run[quad]);
-    mh[quad] = __shfl(st.m_run[quad], (li >> 2) << 4, kWave);
-    lh[quad] = __shfl(l_tot, (li >> 2) << 4, kWave);
+    // (m, l) of head lq: m is the same in the head's 16 lanes, l a per-lane part
+    mh[quad] = st.m_run[quad];
+    lh[quad] = row_sum16(st.l_run[quad]);
     if (G::HALVES == 2 && half == 1) {
       float* dst = xo + ((w * QUADS + quad) * 64 + lane) * 8;
 #pragma unroll
       for (int i = 0; i < 8; ++i) dst[i] = ov[quad][i];
-      if (lq == 0 && (li & 3) == 0) {
-        xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2] = mh[quad];
-        xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2 + 1] = lh[quad];
+      if (li == 0) {
+        xm[((w * QUADS + quad) * 4 + lq) * 2] = mh[quad];
+        xm[((w * QUADS + quad) * 4 + lq) * 2 + 1] = lh[quad];
       }
     }
   }
@@ -640,42 +646,32 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   for (int quad = 0; quad < QUADS; ++quad) {
     // the other half's state (none with one half per stage)
     const float* src = xo + ((w * QUADS + quad) * 64 + lane) * 8;
-    const float mb = G::HALVES == 2 ? xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2] : -INFINITY;
-    const float lb = G::HALVES == 2 ? xm[((w * QUADS + quad) * 4 + (li >> 2)) * 2 + 1] : 0.0f;
+    const float mb = G::HALVES == 2 ? xm[((w * QUADS + quad) * 4 + lq) * 2] : -INFINITY;
+    const float lb = G::HALVES == 2 ? xm[((w * QUADS + quad) * 4 + lq) * 2 + 1] : 0.0f;
     const float ma = mh[quad], la = lh[quad];
     const float mm = fmaxf(ma, mb);
     const float wa = (la > 0.0f) ? exp2f(ma - mm) : 0.0f;
     const float wb2 = (lb > 0.0f) ? exp2f(mb - mm) : 0.0f;
     const float lt = la * wa + lb * wb2;
-    const int hcol = quad * 4 + (li >> 2);
-    if (hcol < p.gq) {
-      float* orow = p.part_o + (prow + hcol) * 128;
-      const int g = li & 3;
-      f32x4 o0, o1;
+    const int hq = quad * 4 + lq;
+    if (hq < p.gq) {
+      float* orow = p.part_o + (prow + hq) * 128;
+      float o[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        o0[i] = wa != 0.0f ? wa * ov[quad][i] : 0.0f;
-        o1[i] = wa != 0.0f ? wa * ov[quad][4 + i] : 0.0f;
-        if (G::HALVES == 2) {
-          o0[i] += wb2 != 0.0f ? wb2 * src[i] : 0.0f;
-          o1[i] += wb2 != 0.0f ? wb2 * src[4 + i] : 0.0f;
-        }
+      for (int k = 0; k < 8; ++k) {
+        o[k] = wa != 0.0f ? wa * ov[quad][k] : 0.0f;
+        if (G::HALVES == 2) o[k] += wb2 != 0.0f ? wb2 * src[k] : 0.0f;
       }
       if (BITS == 4) {
-        // tiles 2g, 2g+1: dims 16n + 4lq + i
-        *reinterpret_cast<f32x4*>(orow + 32 * g + 4 * lq) = o0;
-        *reinterpret_cast<f32x4*>(orow + 32 * g + 16 + 4 * lq) = o1;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) orow[16 * k + li] = o[k];
       } else {
-        // tile 2g + par: dims 32g + 2(4lq + i) + par
-        f32x4 e0, e1;
-        e0[0] = o0[0]; e0[1] = o1[0]; e0[2] = o0[1]; e0[3] = o1[1];
-        e1[0] = o0[2]; e1[1] = o1[2]; e1[2] = o0[3]; e1[3] = o1[3];
-        *reinterpret_cast<f32x4*>(orow + 32 * g + 8 * lq) = e0;
-        *reinterpret_cast<f32x4*>(orow + 32 * g + 8 * lq + 4) = e1;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) *reinterpret_cast<float2*>(orow + 32 * n + 2 * li) = float2{o[2 * n], o[2 * n + 1]};
       }
-      if (lq == 0 && g == 0) {
-        p.part_ml[2 * (prow + hcol)] = lt > 0.0f ? mm : -INFINITY;
-        p.part_ml[2 * (prow + hcol) + 1] = lt;
+      if (li == 0) {
+        p.part_ml[2 * (prow + hq)] = lt > 0.0f ? mm : -INFINITY;
+        p.part_ml[2 * (prow + hq) + 1] = lt;
       }
     }
   }
@@ -693,8 +689,8 @@ int launch_quads(const StagedParams& prm, int grid, int dtype, hipStream_t s) {
     case KVSSD_DTYPE_F16:
       launch_one<BITS, QUADS, 1, _Float16, KG>(prm, grid, s);
       break;
-    case KVSSD_DTYPE_BF16:
-      launch_one<BITS, QUADS, 2, uint16_t, KG>(prm, grid, s);
+    case KVSSD_DTYPE_BF16:  // 8 significant bits: one fp16 part holds a normalised value exactly
+      launch_one<BITS, QUADS, 1, uint16_t, KG>(prm, grid, s);
       break;
     case KVSSD_DTYPE_F32:
       launch_one<BITS, QUADS, 2, float, KG>(prm, grid, s);

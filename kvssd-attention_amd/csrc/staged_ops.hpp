@@ -27,6 +27,16 @@ __device__ __forceinline__ uint32_t pack_half2(_Float16 lo, _Float16 hi) {
          (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, hi)) << 16);
 }
 
+// (fp16(a0 * b0), fp16(a1 * b1)) as one fp16 pair: written as fused
+// multiply-adds of +0 into a two-element vector, the compiler forms each half
+// with one v_fma_mix{lo,hi}_f16 (products of an fp32 and an fp16 value).
+__device__ __forceinline__ uint32_t wpair(float a0, float b0, float a1, float b1) {
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  const half2_t v = {static_cast<_Float16>(__builtin_fmaf(a0, b0, 0.0f)),
+                     static_cast<_Float16>(__builtin_fmaf(a1, b1, 0.0f))};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 __device__ __forceinline__ float half_lo(uint32_t x) { return half_bits_to_float(static_cast<uint16_t>(x & 0xFFFFu)); }
 __device__ __forceinline__ float half_hi(uint32_t x) { return half_bits_to_float(static_cast<uint16_t>(x >> 16)); }
 
@@ -88,13 +98,14 @@ __device__ __forceinline__ void dma4(const uint8_t* sbase, uint32_t voff, uint32
 struct Masks {
   uint32_t m03;  // bits 0-3 of both halves (INT4, F = 1024)
   uint32_t m47;  // bits 4-7 (INT4, F = 64)
-  uint32_t m89;  // bits 8-9 (INT2, F = 4)
+  uint32_t m45;  // bits 4-5 (INT2, F = 64)
   uint32_t m67;  // bits 6-7 (INT2, F = 16)
+  uint32_t m89;  // bits 8-9 (INT2, F = 4)
 };
 
 __device__ __forceinline__ Masks make_masks(uint32_t opaque_zero) {
-  return Masks{0x000F000Fu | opaque_zero, 0x00F000F0u | opaque_zero, 0x03000300u | opaque_zero,
-               0x00C000C0u | opaque_zero};
+  return Masks{0x000F000Fu | opaque_zero, 0x00F000F0u | opaque_zero, 0x00300030u | opaque_zero,
+               0x00C000C0u | opaque_zero, 0x03000300u | opaque_zero};
 }
 
 // (x & m) | 1.0-pairs as one v_bitop3_b32 (truth table 0xEA = (a & b) | c): a
@@ -115,44 +126,61 @@ __device__ __forceinline__ u32x4 unpack4(uint32_t x, const Masks& k) {
 // INT4 slot s holds its code at F = 1024 (else F = 64)
 constexpr bool fine_slot4(int s) { return ((s >> 1) & 1) == 0; }
 
-// INT2 K word x (codes c0..c15, c_j at bits 2j): pairs (c_j, c_{j+8}) for
-// j = o..o+3 (o = 0 or 4); slot s = 2i + hi holds c_{o+i+8hi}.  Even j go to
-// bits 8-9 (F = 4), odd j to bits 6-7 (F = 16): F(s) = (s & 2) ? 16 : 4.
+// INT2 K word x (codes c0..c15, c_j at bits 2j): register i of MFMA step
+// parity o (0 or 1) holds the pair (c_j, c_{j+8}), j = int2_code(o, i), in
+// its two halves (slot s = 2i + hi holds c_{j + 8 hi}).  Every code lands at
+// bits 4-5 (F = 64), 6-7 (F = 16) or 8-9 (F = 4) of its half: c2..c4 are
+// there already, c5..c7 after x >> 6, c0 and c1 after x << 6 -- two shifts
+// per word.  The offset term the accumulator carries grows with F, and its
+// fp32 rounding with it; a score sums 128 dims only, so F = 64 costs nothing
+// measurable (c0 and c1 left at F = 1024 and 256 would save one more shift).
+__host__ __device__ constexpr int int2_code(int o, int i) { return (2 + 4 * o + i) & 7; }
+// c_j sits at bit 4 + 2 ((j + 1) mod 3) of its half
+__host__ __device__ constexpr float int2_f(int j) { return static_cast<float>(64 >> (2 * ((j + 1) % 3))); }
+
 __device__ __forceinline__ u32x4 unpack2(uint32_t x, int o, const Masks& k) {
-  if (o == 0) return u32x4{ao(x << 8, k.m89), ao(x << 4, k.m67), ao(x << 4, k.m89), ao(x, k.m67)};
-  return u32x4{ao(x, k.m89), ao(x >> 4, k.m67), ao(x >> 4, k.m89), ao(x >> 8, k.m67)};
+  const uint32_t r = x >> 6;
+  if (o == 0) return u32x4{ao(x, k.m45), ao(x, k.m67), ao(x, k.m89), ao(r, k.m45)};
+  const uint32_t l = x << 6;
+  return u32x4{ao(r, k.m67), ao(r, k.m89), ao(l, k.m67), ao(l, k.m89)};
 }
 
 // INT2 transpose-read word x (nibble rho = codes of dims 2j, 2j+1 of token
-// row rho): parity 0 takes the even-dim code (bits 4rho..4rho+1) to bits 8-9
-// (F = 4), parity 1 the odd one (bits 4rho+2..4rho+3) to bits 6-7 (F = 16);
-// slot s <-> row (s>>1) + 4(s&1).
+// row rho; slot s <-> row (s>>1) + 4(s&1)): parity 0 takes the even-dim code
+// (bits 4rho..4rho+1) to bits 8-9 (F = 4), parity 1 the odd one to bits 6-7
+// (F = 16); the shifts (8, 4, -4, -8) serve both.  (Parity 0 at bits 4-5
+// would need one shift fewer per word, but at F = 64 the offset the
+// accumulator carries over a split's tokens grows 16-fold, and with it the
+// fp32 rounding: measured 4x the output error on outlier-heavy values.)
 __device__ __forceinline__ u32x4 unpack2_tr(uint32_t x, int parity, const Masks& k) {
   if (parity == 0) return u32x4{ao(x << 8, k.m89), ao(x << 4, k.m89), ao(x, k.m89), ao(x >> 4, k.m89)};
   return u32x4{ao(x << 4, k.m67), ao(x, k.m67), ao(x >> 4, k.m67), ao(x >> 8, k.m67)};
 }
 
-// QK: the query operand of K slot s carries F(s) / G, so every product is
-// q * v(s) * F(s) / G, and the accumulator starts at -sum q' OFF(s);
-// then C = sum q (c - mid) / G.
+// QK: the query operand of MFMA step m's K slot s carries F / G, so every
+// product is q * v * F / G, and the accumulator starts at -sum q' OFF;
+// then C = sum q (c - mid) / G (mid = 8 for INT4, 2 for INT2: OFF = 1 + mid/F).
 template <int BITS>
 constexpr float kQkG = BITS == 4 ? 64.0f : 4.0f;
 template <int BITS>
-__device__ __forceinline__ float qk_factor(int s) {
-  if (BITS == 4) return fine_slot4(s) ? 16.0f : 1.0f;
-  return (s & 2) ? 4.0f : 1.0f;
+__device__ __forceinline__ float slot_f(int m, int s) {
+  if (BITS == 4) return fine_slot4(s) ? 1024.0f : 64.0f;
+  return int2_f(int2_code(m & 1, s >> 1));
 }
 template <int BITS>
-__device__ __forceinline__ float qk_off(int s) {
-  if (BITS == 4) return fine_slot4(s) ? 1.0078125f : 1.125f;
-  return (s & 2) ? 1.125f : 1.5f;
+__device__ __forceinline__ float qk_factor(int m, int s) {
+  return slot_f<BITS>(m, s) / kQkG<BITS>;
+}
+template <int BITS>
+__device__ __forceinline__ float qk_off(int m, int s) {
+  return 1.0f + (BITS == 4 ? 8.0f : 2.0f) / slot_f<BITS>(m, s);
 }
 
 // dim of QK MFMA m's slot s for lane group q
 template <int BITS>
 __device__ __forceinline__ int qk_dim(int m, int q, int s) {
   if (BITS == 4) return 32 * q + 8 * m + (s >> 1) + 4 * (s & 1);
-  return 32 * q + 16 * (m >> 1) + 4 * (m & 1) + (s >> 1) + 8 * (s & 1);
+  return 32 * q + 16 * (m >> 1) + int2_code(m & 1, s >> 1) + 8 * (s & 1);
 }
 
 // PV: INT2 V codes sit at one position per output tile (parity 0: F = 4,
@@ -166,7 +194,7 @@ __device__ __forceinline__ u32x4 off_operand(float off) {
   return u32x4{w, w, w, w};
 }
 __device__ __forceinline__ u32x4 off_operand4() {
-  const _Float16 f = static_cast<_Float16>(qk_off<4>(0)), c = static_cast<_Float16>(qk_off<4>(2));
+  const _Float16 f = static_cast<_Float16>(qk_off<4>(0, 0)), c = static_cast<_Float16>(qk_off<4>(0, 2));
   const uint32_t wf = pack_half2(f, f), wc = pack_half2(c, c);
   return u32x4{wf, wc, wf, wc};
 }
@@ -261,59 +289,9 @@ struct QueryOps {
   float kscale[QUADS];
 };
 
-// Query operands of the kv head whose first query head is head0 (gq query
-// heads per kv head, QUADS = ceil(gq / 4) groups of 4), for QK lane (li, lq).
-template <int BITS, int QUADS, int QSPLIT, typename QT>
-__device__ __forceinline__ void setup_query(QueryOps<QUADS, QSPLIT>& qo, const void* query, int gq, float scale_log2,
-                                            int head0, int li, int lq) {
-#pragma unroll
-  for (int quad = 0; quad < QUADS; ++quad) {
-    // per-head power-of-two normaliser (exact): |q| * 2^-e in [1, 2)
-    const int hrow = quad * 4 + lq;
-    const int hrow_c = hrow < gq ? hrow : gq - 1;
-    float mx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(load_query<QT>(query, (head0 + hrow_c) * 128 + 8 * li + i)));
-    mx = row_max16(mx);
-    int ex = 0;
-    if (mx > 0.0f && isfinite(mx)) {
-      frexpf(mx, &ex);
-      ex -= 1;
-    }
-    qo.kscale[quad] = kQkG<BITS> * scale_log2 * exp2f(static_cast<float>(ex));
-    // A operand: lane row (h', g') = (li/4, li%4), non-zero when g' == lane group
-    const int ha = quad * 4 + (li >> 2);
-    const int ha_c = ha < gq ? ha : gq - 1;
-    const int e_a = __shfl(ex, (li >> 2) << 4, kWave);
-    const bool live = (li & 3) == lq && ha < gq;
-    float part = 0.0f;  // sum over this lane's row entries of (hi + lo) * OFF
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      _Float16 hi[8], lo[8];
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float raw = load_query<QT>(query, (head0 + ha_c) * 128 + qk_dim<BITS>(m, lq, s));
-        const float x = live ? ldexpf(raw, -e_a) * qk_factor<BITS>(s) : 0.0f;
-        hi[s] = static_cast<_Float16>(x);
-        lo[s] = QSPLIT == 2 ? static_cast<_Float16>(x - static_cast<float>(hi[s])) : static_cast<_Float16>(0.0f);
-        part += (static_cast<float>(hi[s]) + static_cast<float>(lo[s])) * qk_off<BITS>(s);
-      }
-      qo.qa[quad][0][m] = u32x4{pack_half2(hi[0], hi[1]), pack_half2(hi[2], hi[3]), pack_half2(hi[4], hi[5]),
-                                pack_half2(hi[6], hi[7])};
-      if (QSPLIT == 2)
-        qo.qa[quad][QSPLIT - 1][m] = u32x4{pack_half2(lo[0], lo[1]), pack_half2(lo[2], lo[3]),
-                                           pack_half2(lo[4], lo[5]), pack_half2(lo[6], lo[7])};
-    }
-    // C init of lane (li, lq), register g: row (h = lq, g) -> the lane holding
-    // that A row's non-zero entries is (li = 4 lq + g, group g)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) qo.qcorr[quad][g] = -__shfl(part, 16 * g + 4 * lq + g, kWave);
-  }
-}
-
-// As setup_query, with every value converted once: the query operands of the
-// kv head are built through LDS scratch of the calling wave
-// (coop_scratch_bytes, 16-byte aligned).  Writer lane L = 16h + 4q + m forms
+// Query operands of a kv head (gq query heads, QUADS = ceil(gq / 4) groups of
+// 4), each value converted once: they are built through LDS scratch of the
+// calling wave (coop_scratch_bytes, 16-byte aligned).  Writer lane L = 16h + 4q + m forms
 // slot group (m, q) of query head h (of each quad) -- the 8 dims
 // qk_dim(m, q, .) -- then every A-operand lane (li, lq) reads its rows back.
 // Stores are unconditional, one slot per lane: a store under a lane condition
@@ -376,10 +354,10 @@ __device__ __forceinline__ void coop_query_build(QueryOps<QUADS, QSPLIT>& qo, co
     float part = 0.0f;  // sum over the slot group of (hi + lo) * OFF
 #pragma unroll
     for (int sl = 0; sl < 8; ++sl) {
-      const float y = ldexpf(x[sl], -ex) * qk_factor<BITS>(sl);
+      const float y = ldexpf(x[sl], -ex) * qk_factor<BITS>(lane & 3, sl);
       hi[sl] = static_cast<_Float16>(y);
       lo[sl] = QSPLIT == 2 ? static_cast<_Float16>(y - static_cast<float>(hi[sl])) : static_cast<_Float16>(0.0f);
-      part += (static_cast<float>(hi[sl]) + static_cast<float>(lo[sl])) * qk_off<BITS>(sl);
+      part += (static_cast<float>(hi[sl]) + static_cast<float>(lo[sl])) * qk_off<BITS>(lane & 3, sl);
     }
     const int slot = ((quad * 4 + h) * 16 + (lane & 15)) * 16;
     *reinterpret_cast<u32x4*>(hi_s + slot) =
