@@ -249,7 +249,13 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
       tr[n] = BITS == 4 ? lds_read_tr4(buf, G::V_OFF + chunk_byte<G::CPT>(t_tr, 4 * w + (n >> 1)) + 8 * (n & 1))
                         : lds_read_tr4(buf, G::V_OFF + chunk_byte<G::CPT>(t_tr, 2 * w + (n >> 1)) + 8 * (n & 1));
   };
-  if constexpr (kEarlyV) read_v();
+  if constexpr (kEarlyV) {
+    read_v();
+    // (keeps the transpose reads here, with the stage's other LDS reads: the
+    // scheduler would otherwise move them after the QK math, and the PV then
+    // waits out their latency)
+    __builtin_amdgcn_sched_barrier(0);
+  }
   // ---------------------------------------------------------------- QK
   f32x4 cc[QUADS][4];
 #pragma unroll
@@ -421,6 +427,11 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // to different XCDs (round robin over 8); every group of split s gets an id
   // with id % 8 == s % 8, so they share one XCD and its L2: the groups read
   // complementary parts of the same 128-byte lines of the scale rows.
+  // (the empty asm takes the pointer arguments into scalar registers here, so
+  // every kernel argument is loaded in one round trip; left to itself the
+  // compiler loads them only after the exit test below, a second round trip
+  // before the first copy can go out)
+  asm volatile("" ::"s"(p.query), "s"(p.pk), "s"(p.pv), "s"(p.sk), "s"(p.sv), "s"(p.valid), "s"(p.table));
   const int groups = p.kv_heads / KG;
   const int xcd = blockIdx.x & 7;
   const int rest = blockIdx.x >> 3;
