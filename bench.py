@@ -196,13 +196,15 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 4.0, gpu_run=None):
+def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 4.0, gpu_run=None, timed=None):
     """The reference's CPU decode (ReferenceAttentionBackend.run: dequantise in
     fp32, gather the GQA heads, softmax, on torch's CPU threads) timed on this
     host's cores over a sample of the workload's blocks: 1 warm-up and 3 timed
     runs, the median reported.  ``gpu_run(ids)`` gives the HIP result over the
-    same sample, checked here against the CPU result at the contract tolerance.
-    The C oracle (float64, OpenMP) over the same sample is a second figure."""
+    same sample, checked here against the CPU result at the contract tolerance;
+    when the sample is the whole step, ``timed`` (the last timed step's out and
+    lse) is checked against it too.  The C oracle (float64, OpenMP) over the
+    same sample is a second figure."""
     import numpy as np
 
     from kvssd.backends import PackedBatch
@@ -255,6 +257,16 @@ def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 4.0,
                   torch.allclose(g_lse.cpu(), lse, atol=2e-3, rtol=1e-2))
         result["gpu_check"] = {"max_abs_out": d_out, "max_abs_lse": d_lse, "tolerance": "atol 2e-3, rtol 1e-2",
                                "blocks": len(sample), "ok": ok}
+    if timed is not None:
+        if len(sample) == len(ids):
+            t_out, t_lse = (x.cpu() for x in timed)
+            result["timed_step_check"] = {
+                "max_abs_out": float((t_out - out).abs().max()), "max_abs_lse": float((t_lse - lse).abs().max()),
+                "tolerance": "atol 2e-3, rtol 1e-2",
+                "ok": bool(torch.allclose(t_out, out, atol=2e-3, rtol=1e-2) and
+                           torch.allclose(t_lse, lse, atol=2e-3, rtol=1e-2))}
+        else:
+            result["timed_step_check"] = {"ok": None, "why": "the CPU sample is smaller than a step"}
     # the C restatement (float64, OpenMP) over the same sample
     c_threads = min(cores, 64)
     arr = {k: v.numpy() for k, v in host.items()}
@@ -715,6 +727,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = start.elapsed_time(end) / args.steps
+    timed_result = (out.clone(), lse.clone())  # the last timed step's output
     # second pass: the split kernel alone, the same K launches back to back
     # between two events on the launch stream: its average duration (plus the
     # dispatch gap between back-to-back launches, ~0.5 us, which rocprof's
@@ -802,7 +815,8 @@ def main() -> int:
 
         arrays = {k: getattr(batches[0], n) for k, n in
                   (("pk", "packed_k"), ("pv", "packed_v"), ("sk", "scales_k"), ("sv", "scales_v"))}
-        line["cpu_baseline"] = cpu_baseline(torch, query, arrays, valid, bits, table, gpu_run=gpu_run)
+        line["cpu_baseline"] = cpu_baseline(torch, query, arrays, valid, bits, table, gpu_run=gpu_run,
+                                            timed=timed_result)
     print(json.dumps(line), flush=True)
     return 0
 
