@@ -37,7 +37,8 @@
 // (c - mid) = F (v - OFF) with OFF = 1 + mid/F (F = 1024 or 64 per slot for
 // INT4, 64, 16 or 4 for INT2; absorbed by the query operand in QK and by W or
 // the output factor in PV).  The offset is removed through the accumulator: QK starts from
-// -sum q' OFF, PV subtracts an extra MFMA of W against OFF.
+// -sum q' OFF, PV subtracts an extra MFMA of W against OFF (for INT2 both
+// parities' OFF in one operand, one per column half).
 //
 // QK (v_mfma_f32_16x16x32_f16): A = query, rows (h, g) = 4 heads x 4 groups,
 //   row (h, g) holding head h masked to group g; B = K codes of a 16-token
@@ -199,7 +200,9 @@ template <int BITS, int QUADS>
 struct WaveState {
   float m_run[QUADS], l_run[QUADS];
   f32x4 acc[QUADS][8];
-  f32x4 corr[QUADS][BITS == 4 ? 1 : 2];
+  // sum over tokens of W * OFF, rows (head, group); INT2 keeps parity 0's OFF
+  // in columns (lanes li) 0-7 and parity 1's in 8-15 of one accumulator
+  f32x4 corr[QUADS];
 };
 
 // One stage of one wave: tokens 64*half .. 64*half + hv - 1 of the stage are valid.
@@ -209,7 +212,7 @@ struct WaveState {
 template <int BITS, int QUADS, int QSPLIT, int KG>
 __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase, int hv, int w, int half, int li,
                                               int lq, const Masks& mk, const QueryOps<QUADS, QSPLIT>& qo,
-                                              const u32x4 (&offa)[BITS == 4 ? 1 : 2], WaveState<BITS, QUADS>& st) {
+                                              const u32x4& offa, WaveState<BITS, QUADS>& st) {
   using G = Geo<BITS, KG>;
   constexpr int KW = BITS == 4 ? 4 : 2;   // K words per lane and tile
   constexpr int NTR = BITS == 4 ? 8 : 4;  // transpose reads (16 / 32 dims each)
@@ -375,9 +378,7 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
 #pragma unroll
     for (int k = 0; k < 8; ++k) st.acc[quad][k][k >> 1] *= alpha;
 #pragma unroll
-    for (int c = 0; c < NPAR; ++c)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) st.corr[quad][c][g] *= alpha;
+    for (int g = 0; g < 4; ++g) st.corr[quad][g] *= alpha;
   }
   // -------------------------------------------------------------------- PV
   if constexpr (!kEarlyV) {
@@ -403,9 +404,7 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int c = 0; c < NPAR; ++c) st.corr[quad][c] = mfma16(wb[quad][kk], offa[c], st.corr[quad][c]);
+    for (int kk = 0; kk < 2; ++kk) st.corr[quad] = mfma16(wb[quad][kk], offa, st.corr[quad]);
 }
 
 template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
@@ -567,13 +566,9 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   static_assert(kWaves * coop_scratch_bytes<QUADS> <= G::STAGE, "query scratch fits a stage buffer");
   // masks in VGPRs: p.units >= 1, so (lane & (p.units >> 30)) is 0 but opaque
   const Masks mk = make_masks(static_cast<uint32_t>(lane) & static_cast<uint32_t>(p.units >> 30));
-  u32x4 offa[BITS == 4 ? 1 : 2];
-  if (BITS == 4) {
-    offa[0] = off_operand4();
-  } else {
-    offa[0] = off_operand(1.5f);                 // parity 0: F = 4
-    offa[BITS == 4 ? 0 : 1] = off_operand(1.125f);  // parity 1: F = 16
-  }
+  // correction operand: INT4, OFF of each K slot; INT2, a column per lane li:
+  // parity 0's OFF (F = 4) in columns 0-7, parity 1's (F = 16) in 8-15
+  const u32x4 offa = BITS == 4 ? off_operand4() : off_operand(li < 8 ? 1.5f : 1.125f);
 
   WaveState<BITS, QUADS> st;
 #pragma unroll
@@ -582,8 +577,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     st.l_run[quad] = 0.0f;
 #pragma unroll
     for (int n = 0; n < 8; ++n) st.acc[quad][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int c = 0; c < (BITS == 4 ? 1 : 2); ++c) st.corr[quad][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    st.corr[quad] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   }
 
   // ------------------------------------------- double-buffered stage loop
@@ -628,12 +622,23 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   float mh[QUADS], lh[QUADS];
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
+    // INT2: this lane's correction column holds one parity's OFF; the other
+    // parity's is in the lane 8 columns away (the same rows: head lq)
+    f32x4 corr_par[2];
+    if constexpr (BITS == 2) {
+      f32x4 other;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) other[g] = __shfl_xor(st.corr[quad][g], 8, kWave);
+      corr_par[0] = li < 8 ? st.corr[quad] : other;
+      corr_par[1] = li < 8 ? other : st.corr[quad];
+    } else {
+      corr_par[0] = corr_par[1] = st.corr[quad];
+    }
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int g = k >> 1;
-      const int c = BITS == 4 ? 0 : (k & 1);
       const float f = BITS == 4 ? 64.0f : ((k & 1) ? 16.0f : 4.0f);
-      ov[quad][k] = f * (st.acc[quad][k][g] - st.corr[quad][c][g]);
+      ov[quad][k] = f * (st.acc[quad][k][g] - corr_par[BITS == 4 ? 0 : (k & 1)][g]);
     }
     // (m, l) of head lq: m is the same in the head's 16 lanes, l a per-lane part
     mh[quad] = st.m_run[quad];

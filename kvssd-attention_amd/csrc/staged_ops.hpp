@@ -185,7 +185,8 @@ __device__ __forceinline__ int qk_dim(int m, int q, int s) {
 
 // PV: INT2 V codes sit at one position per output tile (parity 0: F = 4,
 // parity 1: F = 16), so out = F (C - sum_t W OFF); the correction operand
-// holds OFF in every slot (rows identical).  INT4 V codes sit at F(s) per K
+// holds one OFF per column (its slots alike), parity 0's in columns 0-7 and
+// parity 1's in 8-15, so one MFMA per K step yields both sums.  INT4 V codes sit at F(s) per K
 // slot; W of slot s carries F(s)/64, the correction operand OFF(s), and
 // out = 64 (C - sum_t W' OFF).
 __device__ __forceinline__ u32x4 off_operand(float off) {
