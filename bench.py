@@ -20,8 +20,8 @@ dominant (split) kernel's average duration: a second pass launches the split
 kernel alone K times back to back between two HIP events on its stream.
 ``step_us`` gives p10 / p50 / p90 of single steps (an event pair around each).
 ``pipeline`` times the public Python path, ``KVSSDPipeline.decode`` on layers
-resident in HBM (selection, argument checks, allocation and the fp16 cast
-included), over a store of the workload's shape written to a temporary
+resident in HBM (selection, argument checks and allocation included; the merge
+writes the fp16 output itself), over a store of the workload's shape written to a temporary
 directory.  ``cpu_baseline`` is the reference's CPU decode (the portable
 ``reference`` backend: torch on all host cores) timed over a bounded sample of
 the same blocks, with the HIP result over that sample checked against it at
@@ -137,7 +137,7 @@ def pipeline_leg(torch, dev, tokens: int, bits: int, qh: int, sel, steps: int, w
     """KVSSDPipeline.decode(query, layer, selector) on layers resident in HBM.
 
     The public Python path, host work included (selection, argument checks,
-    output allocation, the fp16 cast): a KVCacheStore of ``layers`` layers of
+    output allocation; the merge stores the fp16 output): a KVCacheStore of ``layers`` layers of
     the workload's shape is written to a temporary directory, every layer is
     made resident, and the steps cycle through the layers (together larger
     than the Infinity Cache) as a decode over a model's layers does."""
@@ -233,8 +233,8 @@ def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 4.0,
     n = int(max(1, min(len(ids), budget_s / max(per_block, 1e-9))))
     sample = ids[:n]
     run(sample)  # warm-up
-    timed = [run(sample) for _ in range(3)]
-    t, out, lse = sorted(timed, key=lambda r: r[0])[1]
+    runs = [run(sample) for _ in range(3)]
+    t, out, lse = sorted(runs, key=lambda r: r[0])[1]
     nbytes = alg_bytes(len(sample), bits)
     result = {
         "value": round(nbytes / t / 1e9, 4),

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define KVSSD_HIP_ABI_VERSION 4
+#define KVSSD_HIP_ABI_VERSION 5
 
 /* Query element types accepted by kvssd_hip_fused_decode (the reference
  * dispatches fp32/fp64/fp16/bf16 queries: csrc/fused_decode.cu:131-133). */
@@ -73,6 +73,12 @@ typedef struct kvssd_decode_desc {
   int32_t num_selected; /* entries in block_table; 0 when there is none */
   int32_t kernel;       /* enum kvssd_kernel */
   double sm_scale;
+  int32_t out_query_dtype; /* 0: out is fp32 (the reference's output);
+                              1: out holds query_dtype elements, each the
+                              fp32 result rounded to nearest even (what the
+                              reference's pipeline does next with
+                              .to(query.dtype), src/kvssd/pipeline.py:165);
+                              lse is fp32 either way */
 } kvssd_decode_desc;
 
 /* ABI version of the loaded library (KVSSD_HIP_ABI_VERSION). */
@@ -91,8 +97,9 @@ int kvssd_hip_decode_workspace_bytes(const kvssd_decode_desc* desc, size_t* byte
  * never KVSSD_KERNEL_AUTO). */
 int kvssd_hip_decode_kernel(const kvssd_decode_desc* desc, int* kernel);
 
-/* Fused decode attention over a packed batch: out fp32 [query_heads, head_dim]
- * (softmax-normalised), lse fp32 [query_heads] (natural-log log-sum-exp of the
+/* Fused decode attention over a packed batch: out [query_heads, head_dim]
+ * (softmax-normalised; fp32, or query_dtype with desc->out_query_dtype = 1),
+ * lse fp32 [query_heads] (natural-log log-sum-exp of the
  * scaled scores).  Replaces kvssd._C.fused_decode (csrc/bindings.cpp:16-41,
  * csrc/fused_decode.cu:92-143) with the semantics of
  * ReferenceAttentionBackend.run (src/kvssd/backends/reference.py:22-50):
@@ -103,7 +110,7 @@ int kvssd_hip_decode_kernel(const kvssd_decode_desc* desc, int* kernel);
  * query_dtype. */
 int kvssd_hip_fused_decode(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k,
                            const uint8_t* packed_v, const uint16_t* scales_k, const uint16_t* scales_v,
-                           const int32_t* valid_tokens, const int32_t* block_table, float* out, float* lse,
+                           const int32_t* valid_tokens, const int32_t* block_table, void* out, float* lse,
                            void* workspace, size_t workspace_bytes, void* stream);
 
 /* kvssd_hip_fused_decode with no workspace argument and no allocation: the
@@ -116,7 +123,7 @@ int kvssd_hip_fused_decode(const kvssd_decode_desc* desc, const void* query, con
  * order them) per GPU. */
 int kvssd_hip_fused_decode_static(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k,
                                   const uint8_t* packed_v, const uint16_t* scales_k, const uint16_t* scales_v,
-                                  const int32_t* valid_tokens, const int32_t* block_table, float* out, float* lse,
+                                  const int32_t* valid_tokens, const int32_t* block_table, void* out, float* lse,
                                   void* stream);
 
 /* Phase 1 of kvssd_hip_fused_decode alone: every split writes its
@@ -132,7 +139,7 @@ int kvssd_hip_decode_partials(const kvssd_decode_desc* desc, const void* query, 
 
 /* Phase 2: merge the split partials left in `workspace` by
  * kvssd_hip_decode_partials for the same `desc` into out / lse. */
-int kvssd_hip_decode_merge(const kvssd_decode_desc* desc, const void* workspace, size_t workspace_bytes, float* out,
+int kvssd_hip_decode_merge(const kvssd_decode_desc* desc, const void* workspace, size_t workspace_bytes, void* out,
                            float* lse, void* stream);
 
 /* Running exact merge of normalised attention chunks, in place:

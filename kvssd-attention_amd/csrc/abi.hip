@@ -52,6 +52,7 @@ int validate(const kvssd_decode_desc* d, int* units) {
   if (d->query_dtype < KVSSD_DTYPE_F16 || d->query_dtype > KVSSD_DTYPE_F64) return arg_error("unsupported query dtype");
   if (d->kernel < KVSSD_KERNEL_AUTO || d->kernel > KVSSD_KERNEL_STAGED) return arg_error("unknown kernel selector");
   if (d->num_selected < 0) return arg_error("num_selected must be >= 0");
+  if (d->out_query_dtype != 0 && d->out_query_dtype != 1) return arg_error("out_query_dtype must be 0 or 1");
   *units = d->num_blocks;
   return 0;
 }
@@ -148,10 +149,13 @@ int static_scratch(void** ptr) {
   return 0;
 }
 
+// Element type of `out`: fp32, or the query's dtype when the caller asks.
+int out_dtype_of(const kvssd_decode_desc& d) { return d.out_query_dtype ? d.query_dtype : KVSSD_DTYPE_F32; }
+
 // Both decode entry points: the split kernel, then (with `out`) the merge.
 int decode_call(const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
                 const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens,
-                const int32_t* block_table, void* workspace, size_t workspace_bytes, float* out, float* lse,
+                const int32_t* block_table, void* workspace, size_t workspace_bytes, void* out, float* lse,
                 void* stream) {
   int units = 0, kernel = 0, splits = 0;
   if (int rc = prepare(desc, block_table, workspace, workspace_bytes, &units, &kernel, &splits)) return rc;
@@ -185,7 +189,8 @@ int decode_call(const kvssd_decode_desc* desc, const void* query, const uint8_t*
            : kernel == KVSSD_KERNEL_MFMA ? launch_mfma(a, plan, parts)
                                          : launch_general(a, plan, parts);
   if (rc != 0 || out == nullptr) return rc;
-  return launch_merge_splits(parts, splits, desc->query_heads, desc->head_dim, out, lse, a.stream);
+  return launch_merge_splits(parts, splits, desc->query_heads, desc->head_dim, out, out_dtype_of(*desc), lse,
+                             a.stream);
 }
 
 }  // namespace
@@ -262,21 +267,21 @@ __attribute__((visibility("default"))) int kvssd_hip_decode_partials(
 
 __attribute__((visibility("default"))) int kvssd_hip_decode_merge(const kvssd_decode_desc* desc,
                                                                   const void* workspace, size_t workspace_bytes,
-                                                                  float* out, float* lse, void* stream) {
+                                                                  void* out, float* lse, void* stream) {
   int units = 0, kernel = 0, splits = 0;
   if (int rc = validate(desc, &units)) return rc;
   if (int rc = units_of_desc(desc, &units)) return rc;
   if (int rc = plan_checked(desc, units, workspace, workspace_bytes, &kernel, &splits)) return rc;
   if (!out || !lse) return arg_error("a required buffer pointer is NULL");
   SplitPartials parts = carve_partials(const_cast<void*>(workspace), splits, desc->query_heads, desc->head_dim);
-  return launch_merge_splits(parts, splits, desc->query_heads, desc->head_dim, out, lse,
+  return launch_merge_splits(parts, splits, desc->query_heads, desc->head_dim, out, out_dtype_of(*desc), lse,
                              static_cast<hipStream_t>(stream));
 }
 
 __attribute__((visibility("default"))) int kvssd_hip_fused_decode(
     const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
     const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens, const int32_t* block_table,
-    float* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+    void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
   if (!out || !lse) return arg_error("a required buffer pointer is NULL");
   return decode_call(desc, query, packed_k, packed_v, scales_k, scales_v, valid_tokens, block_table, workspace,
                      workspace_bytes, out, lse, stream);
@@ -285,7 +290,7 @@ __attribute__((visibility("default"))) int kvssd_hip_fused_decode(
 __attribute__((visibility("default"))) int kvssd_hip_fused_decode_static(
     const kvssd_decode_desc* desc, const void* query, const uint8_t* packed_k, const uint8_t* packed_v,
     const uint16_t* scales_k, const uint16_t* scales_v, const int32_t* valid_tokens, const int32_t* block_table,
-    float* out, float* lse, void* stream) {
+    void* out, float* lse, void* stream) {
   if (!out || !lse) return arg_error("a required buffer pointer is NULL");
   size_t need = 0;
   if (int rc = kvssd_hip_decode_workspace_bytes(desc, &need)) return rc;

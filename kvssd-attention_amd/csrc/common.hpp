@@ -76,6 +76,29 @@ __device__ __forceinline__ float load_query<double>(const void* q, int index) {
   return static_cast<float>(static_cast<const double*>(q)[index]);
 }
 
+// fp32 -> storage of a destination dtype, rounded to nearest even (the
+// rounding of torch's Tensor.to for these types; bf16 NaN -> 0x7FC0)
+template <typename T>
+__device__ __forceinline__ T store_cast(float x);
+template <>
+__device__ __forceinline__ _Float16 store_cast<_Float16>(float x) {
+  return static_cast<_Float16>(x);
+}
+template <>
+__device__ __forceinline__ float store_cast<float>(float x) {
+  return x;
+}
+template <>
+__device__ __forceinline__ double store_cast<double>(float x) {
+  return static_cast<double>(x);
+}
+template <>
+__device__ __forceinline__ uint16_t store_cast<uint16_t>(float x) {  // bfloat16 bits
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;  // NaN
+  return static_cast<uint16_t>((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
+}
+
 // Rows of a block that take part in attention for its count v: the rows
 // Python's slice keys[block, :v] keeps (src/kvssd/backends/reference.py:38-40),
 // i.e. min(v, BT) for v >= 0 and max(BT + v, 0) for v < 0.

@@ -15,8 +15,6 @@ struct DecodeArgs {
   const int32_t* valid;
   const int32_t* table;  // nullptr: identity over num_blocks
   int units;             // blocks attended (num_selected or num_blocks)
-  float* out;
-  float* lse;
   hipStream_t stream;
 };
 
@@ -44,9 +42,10 @@ bool staged_wide(const kvssd_decode_desc& d, int units);
 bool staged_aligned(const DecodeArgs& a);
 int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts);
 
-// ---- split-K phase 2: merge the partials of every split into (out, lse)
-int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, float* out, float* lse,
-                        hipStream_t stream);
+// ---- split-K phase 2: merge the partials of every split into (out, lse);
+// out holds elements of out_dtype (enum kvssd_dtype), lse fp32
+int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, void* out, int out_dtype,
+                        float* lse, hipStream_t stream);
 
 // ---- chunk merge (pipeline), codec twins
 int launch_merge_chunks(int rows, int dim, float* acc_out, float* acc_lse, const float* out, const float* lse,

@@ -4,7 +4,10 @@
 // (O_s unnormalised, m_s in log2 units, l_s = sum 2^(s - m_s)):
 //   M = max_s m_s,  L = sum_s l_s 2^(m_s - M),
 //   out = sum_s O_s 2^(m_s - M) / L,  lse = ln 2 * (M + log2 L),
-// with the weights 2^(m_s - M) formed once per (head, split).
+// with the weights 2^(m_s - M) formed once per (head, split).  `out` is
+// stored as fp32 or, on request, in the query's dtype (one round to nearest
+// even of the fp32 value, what a later Tensor.to(query.dtype) would give);
+// lse stays fp32.
 // Splits with l_s = 0 (no valid token) contribute nothing; if every split is
 // empty, out = 0 and lse = -inf (attention over an empty token set, as
 // src/kvssd/backends/reference.py:46-49 returns it).
@@ -38,10 +41,10 @@ constexpr int kMaxMergeSplits = 2048;
 constexpr int kSliceDims = 16;
 constexpr int kPhases = kWave / kSliceDims;  // 4
 
-template <int OPL, typename OFF>
+template <int OPL, typename OFF, typename OT>
 __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __restrict__ part_o,
                                                             const float* __restrict__ part_ml, int splits,
-                                                            int query_heads, int head_dim, float* __restrict__ out,
+                                                            int query_heads, int head_dim, OT* __restrict__ out,
                                                             float* __restrict__ lse) {
   constexpr int kBatchSplits = kPhases * OPL;
   constexpr int kOPerLane = OPL;
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __rest
     acc = (rescale != 0.0f ? acc * rescale : 0.0f) + osum;
     big_m = m_new;
   }
-  if (ph == 0 && live) out[static_cast<long>(h) * head_dim + d0 + dd] = big_l > 0.0f ? acc / big_l : 0.0f;
+  if (ph == 0 && live) out[static_cast<long>(h) * head_dim + d0 + dd] = store_cast<OT>(big_l > 0.0f ? acc / big_l : 0.0f);
   if (lane == 0 && blockIdx.y == 0) lse[h] = big_l > 0.0f ? kLn2 * (big_m + log2f(big_l)) : -INFINITY;
 }
 
@@ -140,20 +143,41 @@ __global__ __launch_bounds__(kMergeThreads) void merge_chunks_kernel(int dim, fl
 
 }  // namespace
 
-int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, float* out, float* lse,
+template <typename OT>
+void launch_merge_typed(SplitPartials parts, int splits, int query_heads, int head_dim, OT* out, float* lse,
                         hipStream_t stream) {
-  if (splits > kMaxMergeSplits) return arg_error("too many splits for the merge kernel");
   const int slices = (head_dim + kSliceDims - 1) / kSliceDims;
   const dim3 grid(query_heads, slices);
   if (split_partial_bytes(splits, query_heads, head_dim) > 0xFFFFFFFFull)
-    hipLaunchKernelGGL((merge_splits_kernel<16, uint64_t>), grid, dim3(kWave), 0, stream, parts.o, parts.ml, splits,
-                       query_heads, head_dim, out, lse);
+    hipLaunchKernelGGL((merge_splits_kernel<16, uint64_t, OT>), grid, dim3(kWave), 0, stream, parts.o, parts.ml,
+                       splits, query_heads, head_dim, out, lse);
   else if (splits <= kPhases * 16)
-    hipLaunchKernelGGL((merge_splits_kernel<16, uint32_t>), grid, dim3(kWave), 0, stream, parts.o, parts.ml, splits,
-                       query_heads, head_dim, out, lse);
+    hipLaunchKernelGGL((merge_splits_kernel<16, uint32_t, OT>), grid, dim3(kWave), 0, stream, parts.o, parts.ml,
+                       splits, query_heads, head_dim, out, lse);
   else
-    hipLaunchKernelGGL((merge_splits_kernel<64, uint32_t>), grid, dim3(kWave), 0, stream, parts.o, parts.ml, splits,
-                       query_heads, head_dim, out, lse);
+    hipLaunchKernelGGL((merge_splits_kernel<64, uint32_t, OT>), grid, dim3(kWave), 0, stream, parts.o, parts.ml,
+                       splits, query_heads, head_dim, out, lse);
+}
+
+int launch_merge_splits(SplitPartials parts, int splits, int query_heads, int head_dim, void* out, int out_dtype,
+                        float* lse, hipStream_t stream) {
+  if (splits > kMaxMergeSplits) return arg_error("too many splits for the merge kernel");
+  switch (out_dtype) {
+    case KVSSD_DTYPE_F16:
+      launch_merge_typed(parts, splits, query_heads, head_dim, static_cast<_Float16*>(out), lse, stream);
+      break;
+    case KVSSD_DTYPE_BF16:
+      launch_merge_typed(parts, splits, query_heads, head_dim, static_cast<uint16_t*>(out), lse, stream);
+      break;
+    case KVSSD_DTYPE_F32:
+      launch_merge_typed(parts, splits, query_heads, head_dim, static_cast<float*>(out), lse, stream);
+      break;
+    case KVSSD_DTYPE_F64:
+      launch_merge_typed(parts, splits, query_heads, head_dim, static_cast<double*>(out), lse, stream);
+      break;
+    default:
+      return arg_error("unsupported output dtype");
+  }
   return hip_status(hipGetLastError(), "merge_splits launch");
 }
 

@@ -54,26 +54,6 @@ VPlan make_vplan(uint32_t len, const uint8_t* payload) {
   return v;
 }
 
-__device__ __forceinline__ uint32_t f32_bits(float x) { return __builtin_bit_cast(uint32_t, x); }
-
-// fp32 -> storage of the destination dtype, round to nearest even
-template <typename T>
-__device__ __forceinline__ T store_cast(float x);
-template <>
-__device__ __forceinline__ _Float16 store_cast<_Float16>(float x) {
-  return static_cast<_Float16>(x);
-}
-template <>
-__device__ __forceinline__ float store_cast<float>(float x) {
-  return x;
-}
-template <>
-__device__ __forceinline__ uint16_t store_cast<uint16_t>(float x) {  // bfloat16 bits
-  const uint32_t b = f32_bits(x);
-  if ((b & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;  // NaN
-  return static_cast<uint16_t>((b + 0x7FFFu + ((b >> 16) & 1u)) >> 16);
-}
-
 __device__ __forceinline__ float half_to_f32(uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }

@@ -19,7 +19,7 @@ import torch  # noqa: F401  (must precede the library load; see module docstring
 # The in-tree build; KVSSD_HIP_LIBRARY names another build of the same ABI
 # (an instrumented one, say) for the whole process.
 LIB_PATH = Path(os.environ.get("KVSSD_HIP_LIBRARY") or Path(__file__).resolve().parent / "libkvssd_hip.so").resolve()
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3
 KERNEL_AUTO, KERNEL_GENERAL, KERNEL_MFMA, KERNEL_STAGED = 0, 1, 2, 3
@@ -51,6 +51,7 @@ class DecodeDesc(ctypes.Structure):
         ("num_selected", ctypes.c_int32),
         ("kernel", ctypes.c_int32),
         ("sm_scale", ctypes.c_double),
+        ("out_query_dtype", ctypes.c_int32),  # 1: out in the query's dtype, 0: fp32
     ]
 
 

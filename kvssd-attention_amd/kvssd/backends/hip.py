@@ -104,8 +104,17 @@ class HipAttentionBackend:
         batch: PackedBatch,
         sm_scale: float,
         block_table: torch.Tensor | Sequence[int] | None = None,
+        out_dtype: torch.dtype | None = None,
     ) -> tuple[torch.Tensor, torch.Tensor]:
-        """Fused decode; with ``block_table`` attend over those block ids of the batch, in order."""
+        """Fused decode; with ``block_table`` attend over those block ids of the batch, in order.
+
+        ``out`` is fp32 (the reference's output) unless ``out_dtype`` is the
+        query's dtype: then the merge stores it in that dtype, rounded to
+        nearest even -- the values ``out.to(query.dtype)`` would give, without
+        the extra cast kernel.  ``lse`` is fp32 either way."""
+        if out_dtype is not None and out_dtype not in (torch.float32, query.dtype):
+            raise ValueError(f"out_dtype must be torch.float32 or the query's dtype {query.dtype}, got {out_dtype}")
+        typed = out_dtype is not None and out_dtype != torch.float32
         batch.validate(query)
         if query.device.type != "cuda":
             raise ValueError(f"HIP backend requires ROCm GPU tensors, got {query.device.type}")
@@ -124,13 +133,16 @@ class HipAttentionBackend:
         if block_table is not None:
             table = self._table(block_table, batch.packed_k.shape[0], query.device)
         desc = self.describe(query, batch, sm_scale, 0 if table is None else table.numel())
+        desc.out_query_dtype = int(typed)
         q = query.contiguous()
         pk, pv = batch.packed_k.contiguous(), batch.packed_v.contiguous()
         sk, sv = batch.scales_k.contiguous(), batch.scales_v.contiguous()
         valid = batch.valid_tokens.contiguous()
         need, kern = self._plan(lib, desc)
         with torch.cuda.device(query.device):
-            out = torch.empty((query.shape[0], query.shape[1]), dtype=torch.float32, device=query.device)
+            out = torch.empty(
+                (query.shape[0], query.shape[1]), dtype=query.dtype if typed else torch.float32, device=query.device
+            )
             lse = torch.empty((query.shape[0],), dtype=torch.float32, device=query.device)
             work = torch.empty((max(need, 1),), dtype=torch.uint8, device=query.device)
             stream = torch.cuda.current_stream(query.device)

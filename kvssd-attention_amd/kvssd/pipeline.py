@@ -174,7 +174,9 @@ class KVSSDPipeline:
         scale = 1.0 / math.sqrt(query.shape[-1])
         run = self.attention_backend.run
         if getattr(self.attention_backend, "name", None) == "hip":
-            out, _ = run(query, res.batch, scale, block_table=self._table(res, selected))
+            # the merge writes the query's dtype itself (no separate cast)
+            out, _ = run(query, res.batch, scale, block_table=self._table(res, selected), out_dtype=query.dtype)
+            return out
         else:
             rows = [res.row_of[b] for b in selected]
             idx = torch.tensor(rows, dtype=torch.long, device=self.device)

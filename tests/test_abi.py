@@ -50,6 +50,25 @@ def test_argument_errors_are_negative_with_messages():
     assert lib.kvssd_hip_merge_chunks(0, 8, None, None, None, None, None) < 0
 
 
+def test_descriptor_layout_and_output_dtype_flag():
+    # the C struct: ten int32, a double at byte 40, then out_query_dtype at 48
+    # (padded to 56); a zeroed field keeps the fp32 output of earlier callers
+    assert ctypes.sizeof(_native.DecodeDesc) == 56
+    assert _native.DecodeDesc.sm_scale.offset == 40 and _native.DecodeDesc.out_query_dtype.offset == 48
+    lib = _native.load()
+    desc = _native.DecodeDesc(32, 8, 128, 4, 128, 4, 32, 0, 0, 0, 0.1)
+    assert desc.out_query_dtype == 0
+    n = ctypes.c_size_t(0)
+    assert lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(n)) == 0
+    fp32_bytes = n.value
+    desc.out_query_dtype = 1
+    assert lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(n)) == 0
+    assert n.value == fp32_bytes  # the partials do not depend on the output dtype
+    desc.out_query_dtype = 2
+    assert lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(n)) < 0
+    assert "out_query_dtype" in _native.last_error()
+
+
 def test_kernel_choice_is_reported():
     lib = _native.load()
     k = ctypes.c_int(-1)

@@ -407,3 +407,56 @@ def test_staged_eight_kv_heads_gqa8_reversed_table(cuda_device):
     out, lse = HipAttentionBackend("staged").run(query, batch, 0.1)
     ref_out, ref_lse = O.attention(q, pk, pv, sk, sv, valid, 4, 32, 0.1, threads=16)
     check(out, lse, ref_out, ref_lse)
+
+
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16, torch.float32, torch.float64])
+@pytest.mark.parametrize("bits", [2, 4])
+def test_output_in_query_dtype_is_the_rounded_fp32_output(cuda_device, qdtype, bits):
+    """out_dtype=query.dtype stores what out.to(query.dtype) gives, bit for bit
+    (torch rounds fp32 to fp16 / bf16 to nearest even), for every kernel, a
+    merge of more than 64 splits (600 blocks of one kv head) and empty blocks."""
+    cases = [make_batch(61 + bits, 32, 8, 128, 6, 128, bits, 32), make_batch(62, 4, 1, 128, 600, 16, bits, 32)]
+    cases[1] = cases[1][:5] + (np.where(np.arange(600) % 7 == 0, 0, cases[1][5]).astype(np.int32),)
+    for q, pk, pv, sk, sv, valid in cases:
+        query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, qdtype)
+        for kernel in kernels_for(query, batch):
+            backend = HipAttentionBackend(kernel)
+            out32, lse32 = backend.run(query, batch, 0.1)
+            outq, lseq = backend.run(query, batch, 0.1, out_dtype=qdtype)
+            assert out32.dtype == torch.float32 and outq.dtype == qdtype and lseq.dtype == torch.float32
+            assert torch.equal(outq, out32.to(qdtype)), kernel
+            assert torch.equal(lseq, lse32), kernel
+    # no valid token: 0 in every dtype, lse -inf
+    q, pk, pv, sk, sv, _ = cases[0]
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, np.zeros(6, np.int32), bits, 32, qdtype)
+    outq, lseq = HipAttentionBackend("auto").run(query, batch, 0.1, out_dtype=qdtype)
+    assert torch.all(outq == 0) and torch.all(torch.isneginf(lseq))
+    other = torch.bfloat16 if qdtype == torch.float16 else torch.float16
+    with pytest.raises(ValueError, match="out_dtype"):
+        HipAttentionBackend("auto").run(query, batch, 0.1, out_dtype=other)
+
+
+def test_two_phase_entry_points_write_the_query_dtype(cuda_device):
+    """kvssd_hip_decode_partials + kvssd_hip_decode_merge with out_query_dtype=1
+    give the fused call's typed output."""
+    q, pk, pv, sk, sv, valid = make_batch(63, 32, 8, 128, 40, 128, 4, 32)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, 4, 32, torch.bfloat16)
+    backend = HipAttentionBackend("auto")
+    fused, fused_lse = backend.run(query, batch, 0.1, out_dtype=torch.bfloat16)
+    lib = _native.load()
+    desc = backend.describe(query, batch, 0.1)
+    desc.out_query_dtype = 1
+    need = ctypes.c_size_t(0)
+    _native.check(lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(need)), "workspace")
+    work = torch.empty(need.value, dtype=torch.uint8, device=cuda_device)
+    out = torch.empty(32, 128, dtype=torch.bfloat16, device=cuda_device)
+    lse = torch.empty(32, dtype=torch.float32, device=cuda_device)
+    stream = _native.stream_handle(torch.cuda.current_stream(cuda_device))
+    args = [t.data_ptr() for t in (query, batch.packed_k, batch.packed_v, batch.scales_k, batch.scales_v,
+                                   batch.valid_tokens)]
+    _native.check(lib.kvssd_hip_decode_partials(ctypes.byref(desc), *args, None, work.data_ptr(), need.value, stream),
+                  "decode_partials")
+    _native.check(lib.kvssd_hip_decode_merge(ctypes.byref(desc), work.data_ptr(), need.value, out.data_ptr(),
+                                             lse.data_ptr(), stream), "decode_merge")
+    torch.cuda.synchronize()
+    assert torch.equal(out, fused) and torch.equal(lse, fused_lse)
