@@ -38,6 +38,11 @@ COMMON = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # scalar kernel arguments (up to 16 dwords, up to the first struct passed
+    # by value) arrive preloaded in SGPRs at wave launch instead of through a
+    # load from the kernel-argument segment
+    "-mllvm",
+    "-amdgpu-kernarg-preload-count=16",
     "-Wall",
     "-Wno-unused-result",
 ]

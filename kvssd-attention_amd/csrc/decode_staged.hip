@@ -109,9 +109,29 @@ struct StagedParams {
   const int32_t* table;
   float* part_o;
   float* part_ml;
-  int query_heads, kv_heads, block_tokens, num_blocks, units, splits, blocks_per_split, gq;
+  int query_heads, kv_heads, block_tokens, num_blocks, units, blocks_per_split, gq;
   float scale_log2;  // sm_scale * log2(e)
 };
+
+// The kernel's arguments: the first nine (14 dwords: what the first copies
+// need) arrive preloaded in SGPRs at wave launch (the library is built with
+// -amdgpu-kernarg-preload-count), so no copy waits for a kernel-argument
+// load; these 12 dwords come from the kernel-argument segment in two scalar
+// loads issued at entry.  Every dword is used (`splits` only to fill the
+// second load): the compiler reuses the register of a dead dword at once,
+// and writing a load's destination waits for the load.
+struct StagedRest {
+  const int32_t* valid;
+  const int32_t* table;
+  float* part_o;
+  float* part_ml;
+  int query_heads, num_blocks;
+  float scale_log2;
+  int splits;
+};
+// heads argument: kv_heads in bits 0-15, query heads per kv head in 16-23,
+// bit 24 set when there is a block table
+constexpr uint32_t kHasTable = 1u << 24;
 
 // XOR swizzle of a region's chunk index for token t (CPT chunks per token).
 // A token row of 16 or more chunks spans every bank group, so the swizzle
@@ -407,8 +427,41 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
     for (int kk = 0; kk < 2; ++kk) st.corr[quad] = mfma16(wb[quad][kk], offa, st.corr[quad]);
 }
 
+// s_waitcnt vmcnt(BASE + extra), extra in [0, 4] and wave-uniform (a
+// larger value, which the host's kMaxUnits check rules out, waits for BASE)
+template <int BASE>
+__device__ __forceinline__ void wait_copies_left(int extra) {
+  switch (extra) {
+    case 1: __builtin_amdgcn_s_waitcnt(vmcnt_wait(BASE + 1)); break;
+    case 2: __builtin_amdgcn_s_waitcnt(vmcnt_wait(BASE + 2)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(vmcnt_wait(BASE + 3)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(vmcnt_wait(BASE + 4)); break;
+    default: __builtin_amdgcn_s_waitcnt(vmcnt_wait(BASE)); break;
+  }
+}
+
 template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
-__global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p) {
+__global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* query, const uint8_t* pk,
+                                                                 const uint8_t* pv, const uint8_t* sk,
+                                                                 const uint8_t* sv, uint32_t heads, int block_tokens,
+                                                                 int blocks_per_split, int units_total,
+                                                                 StagedRest r) {
+  const StagedParams p{query,           pk,
+                       pv,              sk,
+                       sv,              r.valid,
+                       r.table,         r.part_o,
+                       r.part_ml,       r.query_heads,
+                       static_cast<int>(heads & 0xFFFFu), block_tokens,
+                       r.num_blocks,    units_total,
+                       blocks_per_split, static_cast<int>((heads >> 16) & 0xFFu),
+                       r.scale_log2};
+  const bool has_table = (heads & kHasTable) != 0;
+  // the non-preloaded arguments, in SGPRs from here on (they stay live, so no
+  // register of theirs is reused before this point)
+  auto rest_in_sgprs = [&] {
+    asm volatile("" ::"s"(r.valid), "s"(r.table), "s"(r.part_o), "s"(r.part_ml), "s"(r.query_heads),
+                 "s"(r.num_blocks), "s"(r.scale_log2), "s"(r.splits));
+  };
   using G = Geo<BITS, KG>;
   constexpr int kStage = kStageTok<KG>;
   constexpr int kWBytes = G::W_IN_K ? 0 : kWaves * QUADS * 2048;
@@ -426,18 +479,14 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // to different XCDs (round robin over 8); every group of split s gets an id
   // with id % 8 == s % 8, so they share one XCD and its L2: the groups read
   // complementary parts of the same 128-byte lines of the scale rows.
-  // (the empty asm takes the pointer arguments into scalar registers here, so
-  // every kernel argument is loaded in one round trip; left to itself the
-  // compiler loads them only after the exit test below, a second round trip
-  // before the first copy can go out)
-  asm volatile("" ::"s"(p.query), "s"(p.pk), "s"(p.pv), "s"(p.sk), "s"(p.sv), "s"(p.valid), "s"(p.table));
   const int groups = p.kv_heads / KG;
   const int xcd = blockIdx.x & 7;
   const int rest = blockIdx.x >> 3;
   const int grp = rest % groups;
   const int split = (rest / groups) * 8 + xcd;
-  if (split >= p.splits) return;  // padding ids of the last round
   const int u_begin = split * p.blocks_per_split;
+  // padding ids of the last round (splits = ceil(units / blocks_per_split))
+  if (u_begin >= p.units) return;
   const int u_end = min(p.units, u_begin + p.blocks_per_split);
   const int kvh0 = grp * KG;
   const int head0 = (kvh0 + w) * p.gq;
@@ -451,14 +500,14 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // second stage buffer for the query scratch and the workgroup's query
   // rows): every early memory operation is an LDS copy, so no compiler-placed
   // wait for a load can also wait for a stage.  The query rows go first, then
-  // the split's valid counts (one copy per 64 units) and stage 0; once the
-  // rows and counts land the query operands are built and stage 1 goes out,
+  // stage 0 and the split's valid counts (one copy per 64 units); once the
+  // rows land the query operands are built and stage 1 goes out,
   // before stage 0 has landed: the start is latency-bound, and two stages in
   // flight arrive nearly as soon as one.
   constexpr int kStageCopies = 2 * G::KV_PER_WAVE + 1;    // copy instructions per wave per stage
   constexpr int kQBytesMax = KG * 4 * QUADS * 128 * static_cast<int>(sizeof(QT));
   constexpr bool kEarlyFits = kWaves * coop_scratch_bytes<QUADS> + kQBytesMax <= G::STAGE;
-  const bool direct = kEarlyFits && p.table == nullptr && (reinterpret_cast<uintptr_t>(p.query) & 15u) == 0;
+  const bool direct = kEarlyFits && !has_table && (reinterpret_cast<uintptr_t>(p.query) & 15u) == 0;
   auto advance = [&](Cursor& c) -> bool {
     return direct ? next_stage_direct<kStage>(c, units, u_begin, p.block_tokens, n_units)
                   : next_stage<kStage>(c, units, n_units);
@@ -479,20 +528,25 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     for (int i = wave; i < qcopies; i += kWaves)
       dma16<false>(qsrc, 1024u * static_cast<uint32_t>(i) + 16u * static_cast<uint32_t>(lane),
                    lds_addr(qrows) + 1024u * static_cast<uint32_t>(i));
-    // the split's valid counts, 64 per copy (lanes past the end re-read the last one)
-    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(p.valid + (n_units > 0 ? u_begin : 0));
-    const int ulast = max(n_units - 1, 0);
-    for (int i0 = 64 * wave; i0 < n_units; i0 += 64 * kWaves)
-      dma4(vsrc, 4u * static_cast<uint32_t>(min(i0 + lane, ulast)),
-           lds_addr(reinterpret_cast<const uint8_t*>(units)) + 4u * static_cast<uint32_t>(i0));
     if (n_units > 0) {
       issue_stage<BITS, KG>(p, lds0, Cursor{0, u_begin, 0, 0}, kvh0, wave, cm);
       spec = true;
     }
+    rest_in_sgprs();
+    // the split's valid counts, 64 per copy (lanes past the end re-read the
+    // last one): the only early copies whose address is not preloaded, so
+    // they go last; they are first read once stage 0 has landed
+    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(p.valid + (n_units > 0 ? u_begin : 0));
+    const int ulast = max(n_units - 1, 0);
+    int vcopies = 0;
+    for (int i0 = 64 * wave; i0 < n_units; i0 += 64 * kWaves, ++vcopies)
+      dma4(vsrc, 4u * static_cast<uint32_t>(min(i0 + lane, ulast)),
+           lds_addr(reinterpret_cast<const uint8_t*>(units)) + 4u * static_cast<uint32_t>(i0));
     KVSSD_STAMP(kStampStage0Issued);
-    // the query rows and the valid counts (issued first) have landed once at
-    // most the stage's copies are outstanding (copies complete in issue order)
-    if (spec) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies));
+    // the query rows (issued first) have landed once at most the stage's
+    // copies and the valid counts are outstanding (copies complete in issue
+    // order)
+    if (spec) wait_copies_left<kStageCopies>(vcopies);
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     KVSSD_STAMP(kStampRowsLanded);
@@ -512,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
       if (issued1) issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>(G::STAGE), c1, kvh0, wave, cm);
     }
     KVSSD_STAMP(kStampStage1Issued);
-    // stage 0 and the valid counts landed (stage 1 may still be in flight)
+    // stage 0 and the valid counts landed (only stage 1 may still be in flight)
     if (issued1) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies));
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
@@ -534,6 +588,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
     // The first stage's copies go out before anything else: the split's first
     // attended block, its first stage of tokens (one scalar read with a block
     // table).  If that block holds no valid token they are simply not used.
+    rest_in_sgprs();
     if (u_begin < u_end) {
       Cursor c0{0, __builtin_amdgcn_readfirstlane(p.table ? p.table[u_begin] : u_begin), 0, 0};
       if (c0.blk >= 0 && c0.blk < p.num_blocks) {
@@ -585,7 +640,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
   // copies go out right after the barrier
   int buf = 0;
   bool first = true;
-  int stage_no = 0;
+  [[maybe_unused]] int stage_no = 0;
   KVSSD_STAMP(kStampLoop);
   while (have) {
     if (!first || wait0) {
@@ -695,24 +750,29 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(StagedParams p)
 }
 
 template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
-void launch_one(const StagedParams& prm, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((decode_staged_kernel<BITS, QUADS, QSPLIT, QT, KG>), dim3(grid), dim3(kThreads), 0, s, prm);
+void launch_one(const StagedParams& prm, int splits, int grid, hipStream_t s) {
+  const uint32_t heads = static_cast<uint32_t>(prm.kv_heads) | (static_cast<uint32_t>(prm.gq) << 16) |
+                         (prm.table ? kHasTable : 0u);
+  const StagedRest rest{prm.valid,       prm.table,        prm.part_o,     prm.part_ml,
+                        prm.query_heads, prm.num_blocks,   prm.scale_log2, splits};
+  hipLaunchKernelGGL((decode_staged_kernel<BITS, QUADS, QSPLIT, QT, KG>), dim3(grid), dim3(kThreads), 0, s, prm.query,
+                     prm.pk, prm.pv, prm.sk, prm.sv, heads, prm.block_tokens, prm.blocks_per_split, prm.units, rest);
 }
 
 template <int BITS, int QUADS, int KG>
-int launch_quads(const StagedParams& prm, int grid, int dtype, hipStream_t s) {
+int launch_quads(const StagedParams& prm, int splits, int grid, int dtype, hipStream_t s) {
   switch (dtype) {
     case KVSSD_DTYPE_F16:
-      launch_one<BITS, QUADS, 1, _Float16, KG>(prm, grid, s);
+      launch_one<BITS, QUADS, 1, _Float16, KG>(prm, splits, grid, s);
       break;
     case KVSSD_DTYPE_BF16:  // 8 significant bits: one fp16 part holds a normalised value exactly
-      launch_one<BITS, QUADS, 1, uint16_t, KG>(prm, grid, s);
+      launch_one<BITS, QUADS, 1, uint16_t, KG>(prm, splits, grid, s);
       break;
     case KVSSD_DTYPE_F32:
-      launch_one<BITS, QUADS, 2, float, KG>(prm, grid, s);
+      launch_one<BITS, QUADS, 2, float, KG>(prm, splits, grid, s);
       break;
     case KVSSD_DTYPE_F64:
-      launch_one<BITS, QUADS, 2, double, KG>(prm, grid, s);
+      launch_one<BITS, QUADS, 2, double, KG>(prm, splits, grid, s);
       break;
     default:
       return arg_error("unsupported query dtype");
@@ -721,11 +781,12 @@ int launch_quads(const StagedParams& prm, int grid, int dtype, hipStream_t s) {
 }
 
 template <int KG>
-int launch_kg(const StagedParams& prm, int bits, int dtype, hipStream_t s) {
-  const int grid = 8 * (prm.kv_heads / KG) * ((prm.splits + 7) / 8);
+int launch_kg(const StagedParams& prm, int splits, int bits, int dtype, hipStream_t s) {
+  const int grid = 8 * (prm.kv_heads / KG) * ((splits + 7) / 8);
   const bool two = prm.gq > 4;
-  if (bits == 4) return two ? launch_quads<4, 2, KG>(prm, grid, dtype, s) : launch_quads<4, 1, KG>(prm, grid, dtype, s);
-  return two ? launch_quads<2, 2, KG>(prm, grid, dtype, s) : launch_quads<2, 1, KG>(prm, grid, dtype, s);
+  if (bits == 4)
+    return two ? launch_quads<4, 2, KG>(prm, splits, grid, dtype, s) : launch_quads<4, 1, KG>(prm, splits, grid, dtype, s);
+  return two ? launch_quads<2, 2, KG>(prm, splits, grid, dtype, s) : launch_quads<2, 1, KG>(prm, splits, grid, dtype, s);
 }
 
 }  // namespace
@@ -748,6 +809,7 @@ bool staged_supported(const kvssd_decode_desc& d, std::string* why) {
   if (d.group_size != 32) return no("group_size must be 32");
   if (d.block_tokens % 128) return no("block_tokens must be a multiple of 128");
   if (d.kv_heads % 4) return no("kv_heads must be a multiple of 4");
+  if (d.kv_heads > 0xFFFF) return no("kv_heads must be below 65536");
   const int units = d.num_selected > 0 ? d.num_selected : d.num_blocks;
   if (plan_splits(d, units).blocks_per_split > kMaxUnits) return no("too many blocks per split");
   const int gq = d.query_heads / d.kv_heads;
@@ -777,12 +839,11 @@ int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials part
   prm.block_tokens = d.block_tokens;
   prm.num_blocks = d.num_blocks;
   prm.units = a.units;
-  prm.splits = plan.splits;
   prm.blocks_per_split = plan.blocks_per_split;
   prm.gq = d.query_heads / d.kv_heads;
   prm.scale_log2 = static_cast<float>(d.sm_scale) * kLog2e;
-  if (staged_wide(d, a.units)) return launch_kg<8>(prm, d.bits, d.query_dtype, a.stream);
-  return launch_kg<4>(prm, d.bits, d.query_dtype, a.stream);
+  if (staged_wide(d, a.units)) return launch_kg<8>(prm, plan.splits, d.bits, d.query_dtype, a.stream);
+  return launch_kg<4>(prm, plan.splits, d.bits, d.query_dtype, a.stream);
 }
 
 }  // namespace kvssd
