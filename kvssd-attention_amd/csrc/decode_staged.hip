@@ -769,10 +769,11 @@ int launch_quads(const StagedParams& prm, int splits, int grid, int dtype, hipSt
       launch_one<BITS, QUADS, 1, uint16_t, KG>(prm, splits, grid, s);
       break;
     case KVSSD_DTYPE_F32:
-      launch_one<BITS, QUADS, 2, float, KG>(prm, splits, grid, s);
-      break;
     case KVSSD_DTYPE_F64:
-      launch_one<BITS, QUADS, 2, double, KG>(prm, splits, grid, s);
+      // (staged_wide never picks 8 kv heads for INT4 with two quads here)
+      if constexpr (BITS == 4 && QUADS == 2 && KG == 8) return arg_error("no 8-kv-head form for this query");
+      else if (dtype == KVSSD_DTYPE_F32) launch_one<BITS, QUADS, 2, float, KG>(prm, splits, grid, s);
+      else launch_one<BITS, QUADS, 2, double, KG>(prm, splits, grid, s);
       break;
     default:
       return arg_error("unsupported query dtype");
@@ -794,8 +795,12 @@ int launch_kg(const StagedParams& prm, int splits, int bits, int dtype, hipStrea
 bool staged_wide(const kvssd_decode_desc& d, int units) {
   // all 8 kv heads of a row per workgroup once the context gives every
   // workgroup at least one block: 2048 (kv head, split) work items, 256
-  // workgroups
+  // workgroups.  Not for INT4 with two query quads and a two-part (fp32 /
+  // fp64) query: that form needs more than 256 VGPRs with 8 kv heads (it
+  // spilled), none with 4.
   const int gq = d.kv_heads > 0 ? d.query_heads / d.kv_heads : 0;
+  const bool two_part = d.query_dtype == KVSSD_DTYPE_F32 || d.query_dtype == KVSSD_DTYPE_F64;
+  if (d.bits == 4 && gq > 4 && two_part) return false;
   return d.head_dim == 128 && d.group_size == 32 && (d.bits == 2 || d.bits == 4) && d.kv_heads % 8 == 0 &&
          d.block_tokens % 128 == 0 && gq >= 1 && gq <= 8 && static_cast<long>(units) * d.kv_heads >= 2048;
 }

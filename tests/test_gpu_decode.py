@@ -340,7 +340,9 @@ def test_staged_eight_kv_heads_per_workgroup(cuda_device, bits, qh, kvh):
     valid[-3:] = 0
     ids = [int(i) for i in rng.permutation(nb)[: 2048 // kvh + 40]]
     table = np.array(ids, np.int32)
-    for qdtype in (torch.float32, torch.float16, torch.bfloat16):
+    # (INT4 with 64 query heads and an fp32 / fp64 query takes 4 kv heads per
+    # workgroup: the 8-kv-head form of those would not fit the registers)
+    for qdtype in (torch.float32, torch.float64, torch.float16, torch.bfloat16):
         qq = torch.from_numpy(q).to(qdtype).float().numpy()
         query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, qdtype=qdtype)
         assert HipAttentionBackend("auto").kernel_for(query, batch) == "staged"
