@@ -107,18 +107,6 @@ __device__ __forceinline__ int clamp_valid(int v, int block_tokens) {
   return n < 0 ? 0 : (n > block_tokens ? block_tokens : n);
 }
 
-// Wave-wide reductions over the 64 lanes (result in every lane).
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-  return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
-}
-
 // --- in-register unpack of packed codes into fp16 pairs (magic numbers) ---
 //
 // A code c sits in the mantissa of an fp16 whose exponent field is that of
@@ -187,6 +175,29 @@ __device__ __forceinline__ float row_sum16(float v) {
   v += row_ror<2>(v);
   v += row_ror<1>(v);
   return v;
+}
+
+// Max / sum over the 64 lanes of a wave (every lane active), in every lane:
+// DPP rotations inside each 16-lane row, then the four row results through
+// v_readlane -- VALU only, where a shuffle (ds_bpermute) pays an LDS round
+// trip per step.
+__device__ __forceinline__ float lane_value(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  v = row_max16(v);
+  return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum16(v);
+  return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
+// v from the lane of this lane's quad given by the DPP quad_perm control
+template <int kQuadPerm>
+__device__ __forceinline__ float quad_lane(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kQuadPerm, 0xF, 0xF,
+                                                               false));
 }
 
 }  // namespace kvssd

@@ -26,17 +26,18 @@ constexpr int kMaxMergeSplits = 2048;
 // One single-wave workgroup per (query head, 16-dim slice): a 32-head decode
 // spreads over 256 waves, so every CU pulls a share of the partials.  Splits
 // go in batches of 4 OPL (OPL = 64, or 16 when there are at most 64 splits).
-// Lane (phase, dim) = (lane / 16, lane % 16) owns the O values of splits
+// Lane (dim, phase) = (lane / 4, lane % 4) owns the O values of splits
 // s = phase (mod 4) of one dim (OPL per batch); lane L owns the (m, l) of
 // splits s = L (mod 64) (OPL / 16 per batch).  Every load of a
 // batch goes out at once (indices clamped into range, so that no load sits
 // under a branch; 32-bit offsets from the uniform base, so that 64 loads in
 // flight fit the registers -- 64-bit ones, OFF = uint64_t, only for partials
 // beyond 4 GiB): up to 4 OPL splits cost one round trip to memory.
-// The batch max and L are wave reductions; the weights 2^(m_s - M) go
-// through a per-wave LDS table laid out [phase][j] so that each lane reads
-// its 64 weights with 16 vector reads (one wave writes and reads it: LDS
-// keeps the order, no barrier).  A later batch rescales the running
+// The batch max and L are wave reductions (DPP and lane reads); the weights
+// 2^(m_s - M) go through a per-wave LDS table laid out [phase][j] so that
+// each lane reads its 64 weights with 16 vector reads (one wave writes and
+// reads it: LDS keeps the order, no barrier); a dim's four phases sit in one
+// lane quad and meet by two DPP adds.  A later batch rescales the running
 // (M, L, O) exactly.
 constexpr int kSliceDims = 16;
 constexpr int kPhases = kWave / kSliceDims;  // 4
@@ -53,8 +54,8 @@ __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __rest
   const int h = blockIdx.x;
   const int d0 = blockIdx.y * kSliceDims;
   const int lane = threadIdx.x;
-  const int ph = lane / kSliceDims;
-  const int dd = lane % kSliceDims;
+  const int ph = lane % kPhases;
+  const int dd = lane / kPhases;
   const bool live = d0 + dd < head_dim;
   const OFF dcol = static_cast<OFF>(live ? d0 + dd : d0);
   const uint8_t* ob = reinterpret_cast<const uint8_t*>(part_o);
@@ -62,6 +63,14 @@ __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __rest
   const OFF qh = static_cast<OFF>(query_heads), hd = static_cast<OFF>(head_dim);
   float big_m = -INFINITY, big_l = 0.0f, acc = 0.0f;
   for (int base = 0; base < splits; base += kBatchSplits) {
+    // (m, l) first: the batch max and weights can be formed while the O
+    // values are still arriving
+    float2 ml[kMlPerLane];
+#pragma unroll
+    for (int k = 0; k < kMlPerLane; ++k) {
+      const OFF r = static_cast<OFF>(min(base + lane + kWave * k, splits - 1)) * qh + static_cast<OFF>(h);
+      ml[k] = *reinterpret_cast<const float2*>(mb + 8u * r);
+    }
     float ov[kOPerLane];
 #pragma unroll
     for (int j = 0; j < kOPerLane; ++j) {
@@ -69,14 +78,14 @@ __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __rest
       const OFF r = static_cast<OFF>(s) * qh + static_cast<OFF>(h);
       ov[j] = *reinterpret_cast<const float*>(ob + 4u * (r * hd + dcol));
     }
+    // every load above is issued before any of the math below (the scheduler
+    // would otherwise sink the O loads past the (m, l) wait: two round trips)
+    __builtin_amdgcn_sched_barrier(0);
     float mv[kMlPerLane], lv[kMlPerLane];
 #pragma unroll
     for (int k = 0; k < kMlPerLane; ++k) {
-      const int s = base + lane + kWave * k;
-      const OFF r = static_cast<OFF>(min(s, splits - 1)) * qh + static_cast<OFF>(h);
-      const float2 ml = *reinterpret_cast<const float2*>(mb + 8u * r);
-      mv[k] = ml.x;
-      lv[k] = s < splits ? ml.y : 0.0f;
+      mv[k] = ml[k].x;
+      lv[k] = base + lane + kWave * k < splits ? ml[k].y : 0.0f;
     }
     // M over the non-empty splits seen so far
     float bm = -INFINITY;
@@ -103,9 +112,9 @@ __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __rest
       osum += w4.z != 0.0f ? w4.z * ov[j + 2] : 0.0f;
       osum += w4.w != 0.0f ? w4.w * ov[j + 3] : 0.0f;
     }
-    // sum over the 4 phases: lanes dd, dd + 16, dd + 32, dd + 48
-    osum += __shfl_xor(osum, 16, kWave);
-    osum += __shfl_xor(osum, 32, kWave);
+    // sum over the 4 phases: the lanes of this lane's quad
+    osum += quad_lane<0xB1>(osum);  // quad_perm [1, 0, 3, 2]
+    osum += quad_lane<0x4E>(osum);  // quad_perm [2, 3, 0, 1]
     const float rescale = big_l > 0.0f ? exp2f(big_m - m_new) : 0.0f;
     big_l = big_l * rescale + lsum;
     acc = (rescale != 0.0f ? acc * rescale : 0.0f) + osum;
