@@ -61,23 +61,33 @@ __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __rest
   const uint8_t* ob = reinterpret_cast<const uint8_t*>(part_o);
   const uint8_t* mb = reinterpret_cast<const uint8_t*>(part_ml);
   const OFF qh = static_cast<OFF>(query_heads), hd = static_cast<OFF>(head_dim);
+  // byte offsets: a split index maps to its offset monotonically, so the
+  // clamp to the last split is a min on the offset (one add and one min per
+  // load, no multiply)
+  const OFF o_split = 4u * qh * hd;                         // O bytes per split
+  const OFF o_lane = 4u * (static_cast<OFF>(h) * hd + dcol);  // split 0, this lane's dim
+  const OFF o_last = static_cast<OFF>(splits - 1) * o_split + o_lane;
+  const OFF m_split = 8u * qh;
+  const OFF m_last = static_cast<OFF>(splits - 1) * m_split + 8u * static_cast<OFF>(h);
   float big_m = -INFINITY, big_l = 0.0f, acc = 0.0f;
   for (int base = 0; base < splits; base += kBatchSplits) {
     // (m, l) first: the batch max and weights can be formed while the O
     // values are still arriving
+    // (the empty asm keeps m0 and o0 opaque: otherwise the compiler folds each
+    // load's scalar step back into a per-lane multiply, (base + lane + 64 k) *
+    // m_split, one v_mul_lo_u32 per load)
+    OFF m0 = static_cast<OFF>(base + lane) * m_split + 8u * static_cast<OFF>(h);
+    asm volatile("" : "+v"(m0));
     float2 ml[kMlPerLane];
 #pragma unroll
-    for (int k = 0; k < kMlPerLane; ++k) {
-      const OFF r = static_cast<OFF>(min(base + lane + kWave * k, splits - 1)) * qh + static_cast<OFF>(h);
-      ml[k] = *reinterpret_cast<const float2*>(mb + 8u * r);
-    }
+    for (int k = 0; k < kMlPerLane; ++k)
+      ml[k] = *reinterpret_cast<const float2*>(mb + min(m0 + static_cast<OFF>(kWave * k) * m_split, m_last));
+    OFF o0 = static_cast<OFF>(base + ph) * o_split + o_lane;
+    asm volatile("" : "+v"(o0));
     float ov[kOPerLane];
 #pragma unroll
-    for (int j = 0; j < kOPerLane; ++j) {
-      const int s = min(base + ph + kPhases * j, splits - 1);
-      const OFF r = static_cast<OFF>(s) * qh + static_cast<OFF>(h);
-      ov[j] = *reinterpret_cast<const float*>(ob + 4u * (r * hd + dcol));
-    }
+    for (int j = 0; j < kOPerLane; ++j)
+      ov[j] = *reinterpret_cast<const float*>(ob + min(o0 + static_cast<OFF>(kPhases * j) * o_split, o_last));
     // every load above is issued before any of the math below (the scheduler
     // would otherwise sink the O loads past the (m, l) wait: two round trips)
     __builtin_amdgcn_sched_barrier(0);
