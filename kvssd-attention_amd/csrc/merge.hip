@@ -8,7 +8,9 @@
 // stored as fp32 or, on request, in the query's dtype (one round to nearest
 // even of the fp32 value, what a later Tensor.to(query.dtype) would give);
 // lse stays fp32.
-// Splits with l_s = 0 (no valid token) contribute nothing; if every split is
+// Splits with l_s = 0 (no valid token) contribute nothing: their weight is 0
+// and every decode kernel stores their O row as zeros (partial rows are finite
+// for finite inputs, so weights multiply them directly); if every split is
 // empty, out = 0 and lse = -inf (attention over an empty token set, as
 // src/kvssd/backends/reference.py:46-49 returns it).
 //
@@ -117,17 +119,17 @@ __global__ __launch_bounds__(kWave) void merge_splits_kernel(const float* __rest
 #pragma unroll
     for (int j = 0; j < kOPerLane; j += 4) {
       const float4 w4 = *reinterpret_cast<const float4*>(&sw[ph * kOPerLane + j]);
-      osum += w4.x != 0.0f ? w4.x * ov[j] : 0.0f;
-      osum += w4.y != 0.0f ? w4.y * ov[j + 1] : 0.0f;
-      osum += w4.z != 0.0f ? w4.z * ov[j + 2] : 0.0f;
-      osum += w4.w != 0.0f ? w4.w * ov[j + 3] : 0.0f;
+      osum = __builtin_fmaf(w4.x, ov[j], osum);
+      osum = __builtin_fmaf(w4.y, ov[j + 1], osum);
+      osum = __builtin_fmaf(w4.z, ov[j + 2], osum);
+      osum = __builtin_fmaf(w4.w, ov[j + 3], osum);
     }
     // sum over the 4 phases: the lanes of this lane's quad
     osum += quad_lane<0xB1>(osum);  // quad_perm [1, 0, 3, 2]
     osum += quad_lane<0x4E>(osum);  // quad_perm [2, 3, 0, 1]
     const float rescale = big_l > 0.0f ? exp2f(big_m - m_new) : 0.0f;
     big_l = big_l * rescale + lsum;
-    acc = (rescale != 0.0f ? acc * rescale : 0.0f) + osum;
+    acc = __builtin_fmaf(acc, rescale, osum);
     big_m = m_new;
   }
   if (ph == 0 && live) out[static_cast<long>(h) * head_dim + d0 + dd] = store_cast<OT>(big_l > 0.0f ? acc / big_l : 0.0f);
