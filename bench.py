@@ -161,6 +161,12 @@ def pipeline_leg(torch, dev, tokens: int, bits: int, qh: int, sel, steps: int, w
             pipe.load_resident()
             for i in range(warmup):
                 pipe.decode(query, i % layers, selector)
+            torch.cuda.synchronize()
+            # host cost of a call alone: K calls with nothing waited for
+            t0 = time.perf_counter()
+            for i in range(steps):
+                pipe.decode(query, i % layers, selector)
+            enqueue = (time.perf_counter() - t0) / steps
             stream = torch.cuda.current_stream(dev)
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
@@ -177,6 +183,7 @@ def pipeline_leg(torch, dev, tokens: int, bits: int, qh: int, sel, steps: int, w
     return {
         "us_per_step": round(wall / steps * 1e6, 2),
         "gpu_us_per_step": round(start.elapsed_time(end) * 1e3 / steps, 2),
+        "host_enqueue_us_per_call": round(enqueue * 1e6, 2),
         "path": f"KVSSDPipeline.decode over {layers} HBM-resident layers in turn, "
         f"{'AllBlocks' if sel is None else f'RecentSinkBlocks{tuple(sel)}'}, hip backend, fp16 output",
         "kernel": kernel,

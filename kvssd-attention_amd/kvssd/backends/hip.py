@@ -112,64 +112,20 @@ class HipAttentionBackend:
         query's dtype: then the merge stores it in that dtype, rounded to
         nearest even -- the values ``out.to(query.dtype)`` would give, without
         the extra cast kernel.  ``lse`` is fp32 either way."""
-        if out_dtype is not None and out_dtype not in (torch.float32, query.dtype):
-            raise ValueError(f"out_dtype must be torch.float32 or the query's dtype {query.dtype}, got {out_dtype}")
-        typed = out_dtype is not None and out_dtype != torch.float32
-        batch.validate(query)
-        if query.device.type != "cuda":
-            raise ValueError(f"HIP backend requires ROCm GPU tensors, got {query.device.type}")
-        if batch.packed_k.dtype != torch.uint8 or batch.packed_v.dtype != torch.uint8:
-            raise ValueError("packed KV must be uint8")
-        if batch.scales_k.dtype != torch.float16 or batch.scales_v.dtype != torch.float16:
-            raise ValueError("scales must be float16")
-        if batch.valid_tokens.dtype != torch.int32:
-            raise ValueError("valid_tokens must be int32")
-        if batch.scales_k.shape[:3] != batch.packed_k.shape[:3] or batch.scales_k.shape[3] != (
-            query.shape[1] // batch.group_size
-        ):
-            raise ValueError("scale dimension mismatch")
-        lib = _native.load()
-        table = None
-        if block_table is not None:
-            table = self._table(block_table, batch.packed_k.shape[0], query.device)
-        desc = self.describe(query, batch, sm_scale, 0 if table is None else table.numel())
-        desc.out_query_dtype = int(typed)
-        q = query.contiguous()
-        pk, pv = batch.packed_k.contiguous(), batch.packed_v.contiguous()
-        sk, sv = batch.scales_k.contiguous(), batch.scales_v.contiguous()
-        valid = batch.valid_tokens.contiguous()
-        need, kern = self._plan(lib, desc)
-        with torch.cuda.device(query.device):
-            out = torch.empty(
-                (query.shape[0], query.shape[1]), dtype=query.dtype if typed else torch.float32, device=query.device
-            )
-            lse = torch.empty((query.shape[0],), dtype=torch.float32, device=query.device)
-            work = torch.empty((max(need, 1),), dtype=torch.uint8, device=query.device)
-            stream = torch.cuda.current_stream(query.device)
-            rc = lib.kvssd_hip_fused_decode(
-                ctypes.byref(desc),
-                _ptr(q),
-                _ptr(pk),
-                _ptr(pv),
-                _ptr(sk),
-                _ptr(sv),
-                _ptr(valid),
-                _ptr(table),
-                _ptr(out),
-                _ptr(lse),
-                _ptr(work),
-                work.numel(),
-                _native.stream_handle(stream),
-            )
-        _native.check(rc, "kvssd_hip_fused_decode")
-        name = _native.KERNEL_NAMES[kern]
-        # the library's AUTO demotion for buffers the faster kernels cannot load
-        if name == "staged" and not self._staged_aligned(pk, pv, sk, sv):
-            name = "mfma"
-        if name == "mfma" and not self._mfma_aligned(batch.bits, pk, pv, sk, sv):
-            name = "general"
-        self.last_kernel = name
-        return out, lse
+        return self.prepare(query, batch, sm_scale, block_table, out_dtype)(query)
+
+    def prepare(
+        self,
+        query: torch.Tensor,
+        batch: PackedBatch,
+        sm_scale: float,
+        block_table: torch.Tensor | Sequence[int] | None = None,
+        out_dtype: torch.dtype | None = None,
+    ) -> "PreparedDecode":
+        """Every check and plan of ``run`` for this batch, selection and query
+        shape, done once; calling the result with a query of that shape, dtype
+        and device decodes (what a decode loop over a resident layer repeats)."""
+        return PreparedDecode(self, query, batch, sm_scale, block_table, out_dtype)
 
     def _plan(self, lib, desc: _native.DecodeDesc) -> tuple[int, int]:
         """(workspace bytes, kernel id) of a decode shape, asked of the library once per shape."""
@@ -230,3 +186,96 @@ class HipAttentionBackend:
             rows, dim, _ptr(acc_out), _ptr(acc_lse), _ptr(out), _ptr(lse), _native.stream_handle(stream)
         )
         _native.check(rc, "kvssd_hip_merge_chunks")
+
+
+class PreparedDecode:
+    """One decode shape over one packed batch with its checks, descriptor,
+    device pointers, kernel choice and workspace size fixed at construction
+    (the checks of HipAttentionBackend.run, csrc/bindings.cpp:34-36 and
+    src/kvssd/backends/base.py:29-55).  A call takes a query of the prepared
+    shape, dtype and device and returns (out, lse) like ``run``.
+
+    The split partials go to a workspace kept per stream: calls on one stream
+    are ordered, so each reuses it; calls on another stream get their own.
+    The object holds references to the batch arrays (and block table), so
+    the pointers it passes stay valid while it lives."""
+
+    _MAX_STREAMS = 8
+
+    def __init__(self, backend: HipAttentionBackend, query, batch, sm_scale, block_table, out_dtype):
+        if out_dtype is not None and out_dtype not in (torch.float32, query.dtype):
+            raise ValueError(f"out_dtype must be torch.float32 or the query's dtype {query.dtype}, got {out_dtype}")
+        typed = out_dtype is not None and out_dtype != torch.float32
+        batch.validate(query)
+        if query.device.type != "cuda":
+            raise ValueError(f"HIP backend requires ROCm GPU tensors, got {query.device.type}")
+        if batch.packed_k.dtype != torch.uint8 or batch.packed_v.dtype != torch.uint8:
+            raise ValueError("packed KV must be uint8")
+        if batch.scales_k.dtype != torch.float16 or batch.scales_v.dtype != torch.float16:
+            raise ValueError("scales must be float16")
+        if batch.valid_tokens.dtype != torch.int32:
+            raise ValueError("valid_tokens must be int32")
+        if batch.scales_k.shape[:3] != batch.packed_k.shape[:3] or batch.scales_k.shape[3] != (
+            query.shape[1] // batch.group_size
+        ):
+            raise ValueError("scale dimension mismatch")
+        lib = _native.load()
+        table = None
+        if block_table is not None:
+            table = backend._table(block_table, batch.packed_k.shape[0], query.device)
+        desc = backend.describe(query, batch, sm_scale, 0 if table is None else table.numel())
+        desc.out_query_dtype = int(typed)
+        pk, pv = batch.packed_k.contiguous(), batch.packed_v.contiguous()
+        sk, sv = batch.scales_k.contiguous(), batch.scales_v.contiguous()
+        valid = batch.valid_tokens.contiguous()
+        self._need, kern = backend._plan(lib, desc)
+        name = _native.KERNEL_NAMES[kern]
+        # the library's AUTO demotion for buffers the faster kernels cannot load
+        if name == "staged" and not backend._staged_aligned(pk, pv, sk, sv):
+            name = "mfma"
+        if name == "mfma" and not backend._mfma_aligned(batch.bits, pk, pv, sk, sv):
+            name = "general"
+        self.kernel = name
+        self._backend = backend
+        self._keep = (pk, pv, sk, sv, valid, table)
+        self._desc = desc
+        self._desc_ref = ctypes.byref(desc)
+        self._fn = lib.kvssd_hip_fused_decode
+        self._ptrs = (_ptr(pk), _ptr(pv), _ptr(sk), _ptr(sv), _ptr(valid), _ptr(table))
+        self._device = query.device
+        self._index = _index(query.device)
+        self._qshape = tuple(query.shape)
+        self._qdtype = query.dtype
+        self._out_shape = (query.shape[0], query.shape[1])
+        self._out_dtype = query.dtype if typed else torch.float32
+        self._work: dict[int, torch.Tensor] = {}
+
+    def __call__(self, query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        if tuple(query.shape) != self._qshape or query.dtype != self._qdtype or query.device != self._device:
+            raise ValueError(
+                f"query {tuple(query.shape)} {query.dtype} on {query.device} does not match the prepared decode "
+                f"({self._qshape} {self._qdtype} on {self._device})"
+            )
+        q = query if query.is_contiguous() else query.contiguous()
+        if torch.cuda.current_device() != self._index:
+            with torch.cuda.device(self._index):
+                return self._launch(q)
+        return self._launch(q)
+
+    def _launch(self, q: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        handle = int(torch.cuda.current_stream(self._device).cuda_stream)
+        work = self._work.get(handle)
+        if work is None:
+            if len(self._work) >= self._MAX_STREAMS:
+                self._work.pop(next(iter(self._work)))
+            work = torch.empty((max(self._need, 1),), dtype=torch.uint8, device=self._device)
+            self._work[handle] = work
+        out = torch.empty(self._out_shape, dtype=self._out_dtype, device=self._device)
+        lse = torch.empty((self._out_shape[0],), dtype=torch.float32, device=self._device)
+        rc = self._fn(
+            self._desc_ref, q.data_ptr(), *self._ptrs, out.data_ptr(), lse.data_ptr(), work.data_ptr(), work.numel(),
+            handle,
+        )
+        _native.check(rc, "kvssd_hip_fused_decode")
+        self._backend.last_kernel = self.kernel
+        return out, lse

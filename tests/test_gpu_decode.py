@@ -462,3 +462,36 @@ def test_two_phase_entry_points_write_the_query_dtype(cuda_device):
                                              lse.data_ptr(), stream), "decode_merge")
     torch.cuda.synchronize()
     assert torch.equal(out, fused) and torch.equal(lse, fused_lse)
+
+
+def test_prepared_decode_matches_run(cuda_device):
+    """HipAttentionBackend.prepare: repeated calls (one workspace per stream),
+    a call on a second stream, the typed output and a block table give run's
+    results bit for bit; a query of another shape or dtype is refused."""
+    rng = np.random.default_rng(91)
+    q, pk, pv, sk, sv, valid = make_batch(92, 32, 8, 128, 40, 128, 4, 32)
+    query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, 4, 32, torch.float16)
+    backend = HipAttentionBackend("auto")
+    for table in (None, [int(i) for i in rng.permutation(40)[:17]]):
+        ref_out, ref_lse = backend.run(query, batch, 0.1, block_table=table)
+        prepared = backend.prepare(query, batch, 0.1, block_table=table)
+        for _ in range(3):
+            out, lse = prepared(query)
+            assert torch.equal(out, ref_out) and torch.equal(lse, ref_lse)
+        side = torch.cuda.Stream(cuda_device)
+        side.wait_stream(torch.cuda.current_stream(cuda_device))
+        with torch.cuda.stream(side):
+            out2, lse2 = prepared(query)
+        torch.cuda.current_stream(cuda_device).wait_stream(side)
+        assert torch.equal(out2, ref_out) and torch.equal(lse2, ref_lse)
+        assert len(prepared._work) == 2
+        typed = backend.prepare(query, batch, 0.1, block_table=table, out_dtype=torch.float16)
+        out16, _ = typed(query)
+        assert out16.dtype == torch.float16 and torch.equal(out16, ref_out.to(torch.float16))
+    # a new query of the same shape is decoded afresh
+    other = torch.randn(32, 128, generator=torch.Generator().manual_seed(3)).to(torch.float16).to(cuda_device)
+    assert torch.equal(prepared(other)[0], backend.run(other, batch, 0.1, block_table=table)[0])
+    with pytest.raises(ValueError, match="does not match"):
+        prepared(query.float())
+    with pytest.raises(ValueError, match="does not match"):
+        prepared(query[:16])
