@@ -738,11 +738,21 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
         for (int k = 0; k < 8; ++k) orow[16 * k + li] = o[k];
       } else {
 #pragma unroll
-        for (int n = 0; n < 4; ++n) *reinterpret_cast<float2*>(orow + 32 * n + 2 * li) = float2{o[2 * n], o[2 * n + 1]};
+        // (non-temporal: measured 0.3 µs faster per INT2 step; for INT4 the
+        // same stores made the step 0.2 µs slower)
+        for (int n = 0; n < 4; ++n) {
+          __builtin_nontemporal_store(o[2 * n], orow + 32 * n + 2 * li);
+          __builtin_nontemporal_store(o[2 * n + 1], orow + 32 * n + 2 * li + 1);
+        }
       }
       if (li == 0) {
-        p.part_ml[2 * (prow + hq)] = lt > 0.0f ? mm : -INFINITY;
-        p.part_ml[2 * (prow + hq) + 1] = lt;
+        if constexpr (BITS == 2) {
+          __builtin_nontemporal_store(lt > 0.0f ? mm : -INFINITY, p.part_ml + 2 * (prow + hq));
+          __builtin_nontemporal_store(lt, p.part_ml + 2 * (prow + hq) + 1);
+        } else {
+          p.part_ml[2 * (prow + hq)] = lt > 0.0f ? mm : -INFINITY;
+          p.part_ml[2 * (prow + hq) + 1] = lt;
+        }
       }
     }
   }
