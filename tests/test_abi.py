@@ -177,3 +177,23 @@ def test_static_scratch_decode_rejects_shapes_beyond_its_limit():
                                            None)
     assert rc < 0 and "static scratch" in _native.last_error()
     assert lib.kvssd_hip_fused_decode_static(ctypes.byref(desc), *fake, None, None, None, None) < 0
+
+
+def test_auto_takes_the_matrix_core_kernel_for_small_decodes():
+    # at most 512 (kv head, attended block) pairs: the one-wave matrix-core
+    # kernel under AUTO (it spreads them over every CU); the staged kernel
+    # beyond, and whenever it is asked for
+    lib = _native.load()
+    k = ctypes.c_int(-1)
+
+    def choice(num_blocks, num_selected=0, kernel=_native.KERNEL_AUTO):
+        desc = _native.DecodeDesc(32, 8, 128, num_blocks, 128, 4, 32, 0, num_selected, kernel, 0.1)
+        assert lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(k)) == 0
+        return k.value
+
+    assert choice(32) == _native.KERNEL_MFMA  # 4K tokens: 256 pairs
+    assert choice(64) == _native.KERNEL_MFMA  # 512 pairs
+    assert choice(65) == _native.KERNEL_STAGED
+    assert choice(1024) == _native.KERNEL_STAGED
+    assert choice(2048, num_selected=33) == _native.KERNEL_MFMA  # a 33-block selection of a long context
+    assert choice(32, kernel=_native.KERNEL_STAGED) == _native.KERNEL_STAGED
