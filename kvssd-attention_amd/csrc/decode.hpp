@@ -18,6 +18,31 @@ struct DecodeArgs {
   hipStream_t stream;
 };
 
+// ---- kernel arguments of the matrix-core kernels.  Their first nine
+// arguments (query, pk, pv, sk, sv and the four dwords below: 14 dwords, what
+// the first loads need) arrive preloaded in SGPRs at wave launch (the library
+// is built with -amdgpu-kernarg-preload-count), so no load waits for a
+// kernel-argument fetch; these 12 come from the kernel-argument segment in
+// two scalar loads issued at entry.  Every dword is used (`splits` fills the
+// second load in a kernel that has no use for it): the compiler reuses the
+// register of a dead dword at once, and writing a pending load's destination
+// waits for the load.
+struct DecodeTail {
+  const int32_t* valid;
+  const int32_t* table;
+  float* part_o;
+  float* part_ml;
+  int query_heads, num_blocks;
+  float scale_log2;  // sm_scale * log2(e)
+  int splits;
+};
+// heads argument: kv_heads in bits 0-15, query heads per kv head in 16-23,
+// bit 24 set when there is a block table
+constexpr uint32_t kHasTable = 1u << 24;
+inline uint32_t pack_heads(int kv_heads, int gq, bool has_table) {
+  return static_cast<uint32_t>(kv_heads) | (static_cast<uint32_t>(gq) << 16) | (has_table ? kHasTable : 0u);
+}
+
 // ---- split-K plan, shared by every kernel so the workspace size and the
 // merge depend only on the shape, never on which kernel ran
 struct SplitPlan {

@@ -349,7 +349,20 @@ __device__ __forceinline__ void process(const Stage& st, const Cursor& c, uint8_
 }
 
 template <int BITS, int QUADS, int QSPLIT, typename QT>
-__global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
+__global__ __launch_bounds__(64) void decode_mfma_kernel(const void* query, const uint8_t* pk, const uint8_t* pv,
+                                                        const uint16_t* sk, const uint16_t* sv, uint32_t heads,
+                                                        int block_tokens, int blocks_per_split, int units_total,
+                                                        DecodeTail r) {
+  const MfmaParams p{query,        pk,
+                     pv,           sk,
+                     sv,           r.valid,
+                     r.table,      r.part_o,
+                     r.part_ml,    r.query_heads,
+                     static_cast<int>(heads & 0xFFFFu), block_tokens,
+                     r.num_blocks, units_total,
+                     r.splits,     blocks_per_split,
+                     static_cast<int>((heads >> 16) & 0xFFu), r.scale_log2};
+  const bool has_table = (heads & kHasTable) != 0;
   constexpr float F = kUnpackScale<BITS>;
   constexpr float OFF = kUnpackOffset<BITS>;
   __shared__ __attribute__((aligned(16))) uint8_t v_lds[kSub * 128 * BITS / 8];
@@ -367,17 +380,28 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
   const int rest = bid >> 3;
   const int kvh = rest % p.kv_heads;
   const int split = (rest / p.kv_heads) * 8 + xcd;
-  if (split >= p.splits) return;
   const int u_begin = split * p.blocks_per_split;
+  // padding ids of the last round (splits = ceil(units / blocks_per_split))
+  if (u_begin >= p.units) return;
   const int u_end = min(p.units, u_begin + p.blocks_per_split);
   const int head0 = kvh * p.gq;
 
-  // first sub-block's loads go out before the query set-up
+  // The first sub-block's loads go out before the query set-up.  Without a
+  // block table they go out at entry, before the first block's valid count is
+  // known (a round trip): the split's first block, its first 128 tokens (in
+  // bounds: u_begin < units = num_blocks).  If that sub-block holds no valid
+  // token they are simply replaced.
   Stage s0, s1;
+  const bool spec = !has_table;
+  if (spec) issue_loads<BITS>(s0, p, Cursor{u_begin, u_begin, 0, 0}, kvh, li, lq);
+  // the non-preloaded arguments, in SGPRs from here on (they stay live, so no
+  // register of theirs is reused before this point)
+  asm volatile("" ::"s"(r.valid), "s"(r.table), "s"(r.part_o), "s"(r.part_ml), "s"(r.query_heads),
+               "s"(r.num_blocks), "s"(r.scale_log2), "s"(r.splits));
   Cursor cur{u_begin - 1, 0, 0, 0};
   bool have0 = next_sub(cur, p, u_end);
   Cursor c0 = cur;
-  if (have0) issue_loads<BITS>(s0, p, c0, kvh, li, lq);
+  if (have0 && !(spec && c0.blk == u_begin && c0.sb0 == 0)) issue_loads<BITS>(s0, p, c0, kvh, li, lq);
 
   // ---------------------------------------------------------------- query
   constexpr bool kNormalise = !std::is_same<QT, _Float16>::value;
@@ -522,7 +546,11 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(MfmaParams p) {
 
 template <int BITS, int QUADS, int QSPLIT, typename QT>
 void launch_one(const MfmaParams& prm, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((decode_mfma_kernel<BITS, QUADS, QSPLIT, QT>), dim3(grid), dim3(64), 0, s, prm);
+  const DecodeTail rest{prm.valid,       prm.table,      prm.part_o,     prm.part_ml,
+                        prm.query_heads, prm.num_blocks, prm.scale_log2, prm.splits};
+  hipLaunchKernelGGL((decode_mfma_kernel<BITS, QUADS, QSPLIT, QT>), dim3(grid), dim3(64), 0, s, prm.query, prm.pk,
+                     prm.pv, prm.sk, prm.sv, pack_heads(prm.kv_heads, prm.gq, prm.table != nullptr),
+                     prm.block_tokens, prm.blocks_per_split, prm.units, rest);
 }
 
 template <int BITS, int QUADS>
@@ -556,6 +584,7 @@ bool mfma_supported(const kvssd_decode_desc& d, std::string* why) {
   if (d.head_dim != 128) return no("head_dim must be 128");
   if (d.group_size != 32) return no("group_size must be 32");
   if (d.block_tokens % kSub) return no("block_tokens must be a multiple of 128");
+  if (d.kv_heads > 0xFFFF) return no("kv_heads must be below 65536");
   const int gq = d.query_heads / d.kv_heads;
   if (gq < 1 || gq > 8) return no("at most 8 query heads per kv head");
   return true;

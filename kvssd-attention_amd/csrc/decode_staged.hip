@@ -113,26 +113,6 @@ struct StagedParams {
   float scale_log2;  // sm_scale * log2(e)
 };
 
-// The kernel's arguments: the first nine (14 dwords: what the first copies
-// need) arrive preloaded in SGPRs at wave launch (the library is built with
-// -amdgpu-kernarg-preload-count), so no copy waits for a kernel-argument
-// load; these 12 dwords come from the kernel-argument segment in two scalar
-// loads issued at entry.  Every dword is used (`splits` only to fill the
-// second load): the compiler reuses the register of a dead dword at once,
-// and writing a load's destination waits for the load.
-struct StagedRest {
-  const int32_t* valid;
-  const int32_t* table;
-  float* part_o;
-  float* part_ml;
-  int query_heads, num_blocks;
-  float scale_log2;
-  int splits;
-};
-// heads argument: kv_heads in bits 0-15, query heads per kv head in 16-23,
-// bit 24 set when there is a block table
-constexpr uint32_t kHasTable = 1u << 24;
-
 // XOR swizzle of a region's chunk index for token t (CPT chunks per token).
 // A token row of 16 or more chunks spans every bank group, so the swizzle
 // only permutes its low 4 bits (the same for CPT 16 and 32).
@@ -445,7 +425,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
                                                                  const uint8_t* pv, const uint8_t* sk,
                                                                  const uint8_t* sv, uint32_t heads, int block_tokens,
                                                                  int blocks_per_split, int units_total,
-                                                                 StagedRest r) {
+                                                                 DecodeTail r) {
   const StagedParams p{query,           pk,
                        pv,              sk,
                        sv,              r.valid,
@@ -761,9 +741,8 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
 
 template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
 void launch_one(const StagedParams& prm, int splits, int grid, hipStream_t s) {
-  const uint32_t heads = static_cast<uint32_t>(prm.kv_heads) | (static_cast<uint32_t>(prm.gq) << 16) |
-                         (prm.table ? kHasTable : 0u);
-  const StagedRest rest{prm.valid,       prm.table,        prm.part_o,     prm.part_ml,
+  const uint32_t heads = pack_heads(prm.kv_heads, prm.gq, prm.table != nullptr);
+  const DecodeTail rest{prm.valid,       prm.table,        prm.part_o,     prm.part_ml,
                         prm.query_heads, prm.num_blocks,   prm.scale_log2, splits};
   hipLaunchKernelGGL((decode_staged_kernel<BITS, QUADS, QSPLIT, QT, KG>), dim3(grid), dim3(kThreads), 0, s, prm.query,
                      prm.pk, prm.pv, prm.sk, prm.sv, heads, prm.block_tokens, prm.blocks_per_split, prm.units, rest);
