@@ -309,6 +309,62 @@ def copy_calibration(torch, dev, nbytes: int, steps: int, warmup: int) -> int:
     return 0
 
 
+def launch_floor(torch, dev, steps: int, warmup: int) -> int:
+    """Back-to-back launches of the library's smallest kernel (the code unpack of
+    64 packed bytes, one 256-thread workgroup) on one stream between two events:
+    the per-launch cost every kernel of a decode step pays on this GPU and
+    runtime, whatever its work.  Issued from Python the loop can be host-bound
+    (``host_us_per_launch`` says so), so the same launches are also captured in
+    a graph and replayed."""
+    from kvssd import _native
+
+    lib = _native.load()
+    packed = torch.randint(0, 255, (64,), dtype=torch.uint8, device=dev)
+    codes = torch.empty(64 * 2, dtype=torch.uint8, device=dev)
+
+    def launch(stream) -> None:
+        _native.check(
+            lib.kvssd_hip_unpack_codes(packed.data_ptr(), 4, 64, codes.data_ptr(), _native.stream_handle(stream)),
+            "unpack_codes",
+        )
+
+    stream = torch.cuda.Stream(dev)
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            launch(stream)
+    torch.cuda.synchronize()
+    n = max(steps, 1000)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        t0 = time.perf_counter()
+        start.record(stream)
+        for _ in range(n):
+            launch(stream)
+        end.record(stream)
+        host = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    loop_us = start.elapsed_time(end) * 1e3 / n
+    per_graph = 100
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(per_graph):
+            launch(stream)
+    graph.replay()
+    torch.cuda.synchronize()
+    reps = max(1, n // per_graph)
+    with torch.cuda.stream(stream):
+        start.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    graph_us = start.elapsed_time(end) * 1e3 / (reps * per_graph)
+    print(json.dumps({"launch_floor_us": round(loop_us, 3), "host_us_per_launch": round(host * 1e6 / n, 3),
+                      "graph_node_us": round(graph_us, 3), "launches": n,
+                      "kernel": "unpack_codes_kernel, 64 bytes, one 256-thread workgroup"}), flush=True)
+    return 0
+
+
 def codec(torch, dev, args) -> int:
     """One launch of the record gather (records -> PackedBatch arrays with the
     CRC check) or of the record encoder (fp16 K/V -> records) over one layer
@@ -621,6 +677,11 @@ def main() -> int:
         help="instead of decoding, time a plain device copy of BYTES bytes per step (the reference "
         "reading for scaling rocprof FETCH_SIZE / WRITE_SIZE to bytes)",
     )
+    ap.add_argument(
+        "--launch-floor",
+        action="store_true",
+        help="instead of decoding, time back-to-back launches of the library's smallest kernel",
+    )
     args = ap.parse_args()
     if args.warmup is None:
         args.warmup = 20
@@ -642,6 +703,8 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     if args.copy_calibration:
         return copy_calibration(torch, dev, args.copy_calibration, args.steps, args.warmup)
+    if args.launch_floor:
+        return launch_floor(torch, dev, args.steps, args.warmup)
     if args.workload in HOST_STAGED:
         return host_staged(torch, dev, args)
     if args.workload in CODEC:
