@@ -235,8 +235,12 @@ def cpu_baseline(torch, query, cache, valid, bits, table, budget_s: float = 4.0,
         out, lse = backend.run(q, batch, scale)
         return time.perf_counter() - t0, out, lse
 
-    # size the sample from a 16-block probe so a run takes about budget_s
-    per_block = run(ids[: min(16, len(ids))])[0] / min(16, len(ids))
+    # size the sample from a 16-block probe so a run takes about budget_s (the
+    # probe's first call pays torch's one-time costs, several times a block's
+    # time, so it is timed on its second call)
+    probe = ids[: min(16, len(ids))]
+    run(probe)
+    per_block = run(probe)[0] / len(probe)
     n = int(max(1, min(len(ids), budget_s / max(per_block, 1e-9))))
     sample = ids[:n]
     run(sample)  # warm-up
