@@ -263,7 +263,10 @@ class PreparedDecode:
         return self._launch(q)
 
     def _launch(self, q: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        handle = int(torch.cuda.current_stream(self._device).cuda_stream)
+        # the current stream's raw handle, without building a Stream object
+        # (torch's own generated code reads it the same way; ~0.2 against
+        # ~1.9 us per call)
+        handle = torch._C._cuda_getCurrentRawStream(self._index)
         work = self._work.get(handle)
         if work is None:
             if len(self._work) >= self._MAX_STREAMS:

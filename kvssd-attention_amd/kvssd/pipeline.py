@@ -159,7 +159,7 @@ class KVSSDPipeline:
 
     def _table(self, res: _Resident, selected: list[int]) -> torch.Tensor | None:
         """Device block table for ``selected``; None when it is every row in order."""
-        if selected == res.ids:
+        if selected is res.ids or selected == res.ids:
             return None
         key = tuple(selected)
         table = res.tables.get(key)
@@ -206,7 +206,14 @@ class KVSSDPipeline:
         selector: BlockSelector | None = None,
     ) -> torch.Tensor:
         selector = selector or AllBlocks()
-        selected = selector.select(self.store.blocks_for_layer(layer))
+        res = self._resident.get(layer)
+        if res is not None and type(selector) is AllBlocks:
+            # every block of an HBM-resident layer, in the store's order: its
+            # batch's row order (a store's block lists never change), with no
+            # copy or compare of the id list on the per-call path
+            selected = res.ids
+        else:
+            selected = selector.select(self.store.blocks_for_layer(layer))
         if not selected:
             raise ValueError("selector returned no blocks")
         query = query.to(self.device)
