@@ -63,9 +63,12 @@ int validate(const kvssd_decode_desc* d, int* units) {
 // workgroup below 2048 pairs) leaves most CUs idle.  Measured per step, 4K
 // tokens: 8.7 against 9.7 us (GQA 4), 10.7 against 11.4 us (GQA 8); GQA 8
 // with a 33-block table: 11.6 against 12.4 us; the two are even near 512
-// pairs and the staged kernel wins from ~768 on.  (Not for INT4 with more than
-// 4 query heads per kv head and a two-part fp32 / fp64 query: that form of the
-// matrix-core kernel spills registers, the staged one does not.)
+// pairs and the staged kernel wins from ~768 on.  At this size the
+// matrix-core kernel gives each query quad of a kv head a workgroup of its
+// own (GQA 8, split kernel: 4K 8.0 -> 7.1 us, the 33-block table 9.0 -> 8.0
+// us), so its two-quad form -- which spills registers with a two-part fp32 /
+// fp64 query -- never runs here (fp32 GQA 8: 7.8 against the staged kernel's
+// 10.0 us).
 constexpr long kSmallPairs = 512;
 
 // Kernel for a shape (pointer alignment can still demote STAGED -> MFMA ->
@@ -85,9 +88,7 @@ int choose_kernel(const kvssd_decode_desc& d, int* kernel) {
     *kernel = KVSSD_KERNEL_GENERAL;
   } else {
     const long units = d.num_selected > 0 ? d.num_selected : d.num_blocks;
-    const bool two_part = d.query_dtype == KVSSD_DTYPE_F32 || d.query_dtype == KVSSD_DTYPE_F64;
-    const bool spills = d.bits == 4 && d.query_heads > 4 * d.kv_heads && two_part;
-    const bool small = units * d.kv_heads <= kSmallPairs && !spills;
+    const bool small = units * d.kv_heads <= kSmallPairs;
     *kernel = staged && !small ? KVSSD_KERNEL_STAGED : mfma ? KVSSD_KERNEL_MFMA : KVSSD_KERNEL_GENERAL;
   }
   return 0;

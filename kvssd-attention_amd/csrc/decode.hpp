@@ -37,10 +37,13 @@ struct DecodeTail {
   int splits;
 };
 // heads argument: kv_heads in bits 0-15, query heads per kv head in 16-23,
-// bit 24 set when there is a block table
+// bit 24 set when there is a block table, bit 25 when each of a kv head's two
+// query quads gets a workgroup of its own (the matrix-core kernel)
 constexpr uint32_t kHasTable = 1u << 24;
-inline uint32_t pack_heads(int kv_heads, int gq, bool has_table) {
-  return static_cast<uint32_t>(kv_heads) | (static_cast<uint32_t>(gq) << 16) | (has_table ? kHasTable : 0u);
+constexpr uint32_t kQuadPerGroup = 1u << 25;
+inline uint32_t pack_heads(int kv_heads, int gq, bool has_table, bool quad_per_group = false) {
+  return static_cast<uint32_t>(kv_heads) | (static_cast<uint32_t>(gq) << 16) | (has_table ? kHasTable : 0u) |
+         (quad_per_group ? kQuadPerGroup : 0u);
 }
 
 // ---- split-K plan, shared by every kernel so the workspace size and the

@@ -5,7 +5,10 @@
 // src/kvssd/backends/reference.py:22-50; element addressing of
 // csrc/fused_decode.cu:50-56).  One wave owns (kv head, range of blocks) and
 // streams 128-token sub-blocks; the packed rows of the kv head are read once
-// and shared by all its query heads.
+// and shared by all its query heads -- or, with more than 4 query heads per kv
+// head on a grid small enough to be resident at once, one wave per (kv head,
+// query quad, range of blocks), each reading the rows (the second one mostly
+// from L2) for half the math.
 //
 // Code -> fp16 without a dequantised tensor: a code c placed in the mantissa of
 // 1.0 gives v = 1 + c/F (F = 64 for INT4, 4 for INT2; common.hpp), and
@@ -65,6 +68,9 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 constexpr int kSub = 128;           // tokens per sub-block
 constexpr int kTiles = kSub / 16;   // QK tiles per sub-block
 constexpr int kWRow = 272;          // bytes per W row: 128 fp16 slots + 16 B pad
+// one-wave workgroups resident at once at one wave per SIMD (256 CUs x 4 SIMDs;
+// the kernel's registers allow no more)
+constexpr long kMfmaResidentWaves = 1024;
 
 struct MfmaParams {
   const void* query;
@@ -374,17 +380,26 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(const void* query, cons
 
   // XCD-aware placement: consecutive workgroup ids go to different XCDs; the
   // kv heads of one split (which share 128-byte lines of the packed rows) get
-  // ids 8 apart, i.e. the same XCD and its L2.
+  // ids 8 apart, i.e. the same XCD and its L2.  With a workgroup per query
+  // quad (kQuadPerGroup; QUADS == 1, more than 4 query heads per kv head) the
+  // two quads of a kv head come next to each other in that order, so the
+  // second reads the kv head's codes from the same L2.
   const int bid = blockIdx.x;
   const int xcd = bid & 7;
   const int rest = bid >> 3;
-  const int kvh = rest % p.kv_heads;
-  const int split = (rest / p.kv_heads) * 8 + xcd;
+  const int qshift = (heads & kQuadPerGroup) ? 1 : 0;
+  const int slots = p.kv_heads << qshift;  // workgroups per split
+  const int slot = rest % slots;
+  const int kvh = slot >> qshift;
+  const int quad0 = slot & qshift;  // this workgroup's first query quad
+  const int split = (rest / slots) * 8 + xcd;
   const int u_begin = split * p.blocks_per_split;
   // padding ids of the last round (splits = ceil(units / blocks_per_split))
   if (u_begin >= p.units) return;
   const int u_end = min(p.units, u_begin + p.blocks_per_split);
-  const int head0 = kvh * p.gq;
+  // this workgroup's query heads: gqw heads from head0 (head0 + 4 quad ...)
+  const int head0 = kvh * p.gq + 4 * quad0;
+  const int gqw = min(p.gq - 4 * quad0, 4 * QUADS);
 
   // The first sub-block's loads go out before the query set-up.  Without a
   // block table they go out at entry, before the first block's valid count is
@@ -412,7 +427,7 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(const void* query, cons
   for (int quad = 0; quad < QUADS; ++quad) {
     // per-head power-of-two normaliser (exact); fp16 queries are used as is
     const int hrow = quad * 4 + lq;  // head of this lane's QK row
-    const int hrow_c = hrow < p.gq ? hrow : p.gq - 1;
+    const int hrow_c = hrow < gqw ? hrow : gqw - 1;
     float e_row = 0.0f;
     if (kNormalise) {
       float mx = 0.0f;
@@ -429,9 +444,9 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(const void* query, cons
     kscale[quad] = F * p.scale_log2 * exp2f(e_row);
     // A operand: lane row (h', g') = (li/4, li%4), non-zero when g' == lane group
     const int ha = quad * 4 + (li >> 2);
-    const int ha_c = ha < p.gq ? ha : p.gq - 1;  // in-range head for unused rows
+    const int ha_c = ha < gqw ? ha : gqw - 1;  // in-range head for unused rows
     const float e_a = __shfl(e_row, (li >> 2) << 4, kWave);
-    const bool live = (li & 3) == lq && ha < p.gq;
+    const bool live = (li & 3) == lq && ha < gqw;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       _Float16 hi[8], lo[8];
@@ -501,13 +516,13 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(const void* query, cons
     wtot += __shfl_xor(wtot, 16, kWave);
     wtot += __shfl_xor(wtot, 32, kWave);
     const int hrow = quad * 4 + lq;
-    if (li == 0 && hrow < p.gq) {
+    if (li == 0 && hrow < gqw) {
       p.part_ml[2 * (prow + hrow)] = qs[quad].m_run;
       p.part_ml[2 * (prow + hrow) + 1] = l_tot;
     }
     const int hcol = quad * 4 + (li >> 2);
     const int g = li & 3;
-    if (hcol < p.gq) {
+    if (hcol < gqw) {
       float* orow = p.part_o + (prow + hcol) * 128;
       // out = F * (C - OFF * sum W) on the tiles whose dims lie in group g;
       // compile-time tile indices keep the accumulators in registers
@@ -545,28 +560,28 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(const void* query, cons
 }
 
 template <int BITS, int QUADS, int QSPLIT, typename QT>
-void launch_one(const MfmaParams& prm, int grid, hipStream_t s) {
+void launch_one(const MfmaParams& prm, int grid, bool quad_per_group, hipStream_t s) {
   const DecodeTail rest{prm.valid,       prm.table,      prm.part_o,     prm.part_ml,
                         prm.query_heads, prm.num_blocks, prm.scale_log2, prm.splits};
   hipLaunchKernelGGL((decode_mfma_kernel<BITS, QUADS, QSPLIT, QT>), dim3(grid), dim3(64), 0, s, prm.query, prm.pk,
-                     prm.pv, prm.sk, prm.sv, pack_heads(prm.kv_heads, prm.gq, prm.table != nullptr),
+                     prm.pv, prm.sk, prm.sv, pack_heads(prm.kv_heads, prm.gq, prm.table != nullptr, quad_per_group),
                      prm.block_tokens, prm.blocks_per_split, prm.units, rest);
 }
 
 template <int BITS, int QUADS>
-int launch_quads(const MfmaParams& prm, int grid, int dtype, hipStream_t s) {
+int launch_quads(const MfmaParams& prm, int grid, bool quad_per_group, int dtype, hipStream_t s) {
   switch (dtype) {
     case KVSSD_DTYPE_F16:
-      launch_one<BITS, QUADS, 1, _Float16>(prm, grid, s);
+      launch_one<BITS, QUADS, 1, _Float16>(prm, grid, quad_per_group, s);
       break;
     case KVSSD_DTYPE_BF16:  // 8 significant bits: one fp16 part holds a normalised value exactly
-      launch_one<BITS, QUADS, 1, uint16_t>(prm, grid, s);
+      launch_one<BITS, QUADS, 1, uint16_t>(prm, grid, quad_per_group, s);
       break;
     case KVSSD_DTYPE_F32:
-      launch_one<BITS, QUADS, 2, float>(prm, grid, s);
+      launch_one<BITS, QUADS, 2, float>(prm, grid, quad_per_group, s);
       break;
     case KVSSD_DTYPE_F64:
-      launch_one<BITS, QUADS, 2, double>(prm, grid, s);
+      launch_one<BITS, QUADS, 2, double>(prm, grid, quad_per_group, s);
       break;
     default:
       return arg_error("unsupported query dtype");
@@ -617,13 +632,19 @@ int launch_mfma(const DecodeArgs& a, const SplitPlan& plan, SplitPartials parts)
   prm.blocks_per_split = plan.blocks_per_split;
   prm.gq = d.query_heads / d.kv_heads;
   prm.scale_log2 = static_cast<float>(d.sm_scale) * kLog2e;
-  // ids cover 8 XCD lanes x kv heads x ceil(splits / 8); surplus ids exit at once
-  const int grid = 8 * d.kv_heads * ((plan.splits + 7) / 8);
+  // More than 4 query heads per kv head: a workgroup per query quad (the
+  // one-quad code, half the math per wave) while the doubled grid still fits
+  // the GPU's SIMDs at one wave each, so every workgroup starts at once and the
+  // codes read twice come from L2 or cost no time on a latency-bound decode;
+  // beyond that one workgroup carries both quads and reads the codes once.
   const bool two = prm.gq > 4;
-  if (d.bits == 4) return two ? launch_quads<4, 2>(prm, grid, d.query_dtype, a.stream)
-                              : launch_quads<4, 1>(prm, grid, d.query_dtype, a.stream);
-  return two ? launch_quads<2, 2>(prm, grid, d.query_dtype, a.stream)
-             : launch_quads<2, 1>(prm, grid, d.query_dtype, a.stream);
+  const bool quad_per_group = two && 2L * plan.splits * d.kv_heads <= kMfmaResidentWaves;
+  // ids cover 8 XCD lanes x workgroups per split x ceil(splits / 8); surplus ids exit at once
+  const int grid = 8 * d.kv_heads * (quad_per_group ? 2 : 1) * ((plan.splits + 7) / 8);
+  if (d.bits == 4) return two && !quad_per_group ? launch_quads<4, 2>(prm, grid, false, d.query_dtype, a.stream)
+                                                 : launch_quads<4, 1>(prm, grid, quad_per_group, d.query_dtype, a.stream);
+  return two && !quad_per_group ? launch_quads<2, 2>(prm, grid, false, d.query_dtype, a.stream)
+                                : launch_quads<2, 1>(prm, grid, quad_per_group, d.query_dtype, a.stream);
 }
 
 }  // namespace kvssd

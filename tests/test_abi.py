@@ -197,9 +197,11 @@ def test_auto_takes_the_matrix_core_kernel_for_small_decodes():
     assert choice(1024) == _native.KERNEL_STAGED
     assert choice(2048, num_selected=33) == _native.KERNEL_MFMA  # a 33-block selection of a long context
     assert choice(32, kernel=_native.KERNEL_STAGED) == _native.KERNEL_STAGED
-    # INT4, 8 query heads per kv head, fp32 query: the matrix-core form of that
-    # spills registers, so it stays on the staged kernel
-    desc = _native.DecodeDesc(64, 8, 128, 32, 128, 4, 32, _native.DTYPE_F32, 0, 0, 0.1)
-    assert lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(k)) == 0 and k.value == _native.KERNEL_STAGED
-    desc.query_dtype = _native.DTYPE_F16
-    assert lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(k)) == 0 and k.value == _native.KERNEL_MFMA
+    # 8 query heads per kv head, any query dtype: small decodes give each query
+    # quad a workgroup of its own, so the two-quad form (which spills with a
+    # two-part fp32 query) is not involved and the matrix-core kernel is taken
+    for dtype in (_native.DTYPE_F32, _native.DTYPE_F16, _native.DTYPE_F64):
+        desc = _native.DecodeDesc(64, 8, 128, 32, 128, 4, 32, dtype, 0, 0, 0.1)
+        assert lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(k)) == 0 and k.value == _native.KERNEL_MFMA
+        desc.num_blocks = 65
+        assert lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(k)) == 0 and k.value == _native.KERNEL_STAGED
