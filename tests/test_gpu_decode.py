@@ -411,6 +411,29 @@ def test_staged_eight_kv_heads_gqa8_reversed_table(cuda_device):
     check(out, lse, ref_out, ref_lse)
 
 
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize(("qh", "kvh", "nb"), [(48, 8, 12), (20, 4, 9), (64, 8, 80), (28, 4, 150)])
+def test_mfma_query_quads_with_and_without_a_workgroup_each(cuda_device, bits, qh, kvh, nb):
+    # More than 4 query heads per kv head (GQA 6, 5, 8, 7) on the matrix-core
+    # kernel.  While 2 x splits x kv heads <= 1024 (one-block splits here),
+    # each query quad gets a workgroup of its own, the second quad only partly
+    # filled for GQA 5-7.  Beyond that (80 x 8 and 150 x 4 splits, with or
+    # without a table) one workgroup carries both quads, the fp32 / fp64 INT4
+    # form with registers spilled.  Every query dtype, empty blocks included.
+    rng = np.random.default_rng(500 + bits + qh + nb)
+    q, pk, pv, sk, sv, _ = make_batch(71 + nb, qh, kvh, 128, nb, 128, bits, 32)
+    valid = rng.integers(0, 129, nb).astype(np.int32)
+    ids = [int(i) for i in rng.permutation(nb)[: max(1, nb - 3)]]
+    for qdtype in (torch.float16, torch.bfloat16, torch.float32, torch.float64):
+        qq = torch.from_numpy(q).to(qdtype).float().numpy()
+        query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, qdtype=qdtype)
+        for selection in (None, ids):
+            table = None if selection is None else np.array(selection, np.int32)
+            ref_out, ref_lse = O.attention(qq, pk, pv, sk, sv, valid, bits, 32, 0.1, block_table=table, threads=16)
+            out, lse = HipAttentionBackend("mfma").run(query, batch, 0.1, block_table=selection)
+            check(out, lse, ref_out, ref_lse)
+
+
 @pytest.mark.parametrize("qdtype", [torch.float16, torch.bfloat16, torch.float32, torch.float64])
 @pytest.mark.parametrize("bits", [2, 4])
 def test_output_in_query_dtype_is_the_rounded_fp32_output(cuda_device, qdtype, bits):
