@@ -37,3 +37,40 @@ def test_decode_over_selections_matches_the_oracle(tmp_path: Path, io_depth: int
                                         block_table=ids)
                 np.testing.assert_allclose(out.numpy(), expect, atol=2e-5, rtol=2e-5)
     store.close()
+
+
+def test_resident_all_blocks_fast_path_selects_what_the_selector_would(tmp_path: Path):
+    # A resident layer decoded under plain AllBlocks takes the batch's row order
+    # as its selection without copying the id list; any other selector,
+    # AllBlocks subclasses included, still goes through its own select().  The
+    # layer is placed in the resident table on CPU tensors here, so the
+    # portable backend serves the decode.
+    from kvssd.backends import PackedBatch
+    from kvssd.pipeline import _Resident
+
+    gen = torch.Generator().manual_seed(91)
+    keys = torch.randn(1, 75, 2, 32, generator=gen)
+    values = torch.randn(1, 75, 2, 32, generator=gen)
+    store = KVCacheStore.create(tmp_path, keys, values, CacheSpec(1, 2, 32, block_tokens=8, bits=4, group_size=16))
+    query = torch.randn(4, 32, generator=gen, dtype=torch.float64)
+    pk, sk, valid = O.quantize_blocks(keys[0].numpy(), 4, 16, 8)
+    pv, sv, _ = O.quantize_blocks(values[0].numpy(), 4, 16, 8)
+    ids = store.blocks_for_layer(0)
+    assert ids == list(range(10))
+    batch = PackedBatch(*(torch.from_numpy(a) for a in (pk, pv, sk, sv, valid)), 4, 16)
+
+    class FirstTwo(AllBlocks):
+        def select(self, available):
+            return list(available)[:2]
+
+    scale = 1 / math.sqrt(32)
+    with KVSSDPipeline(store, device="cpu") as pipe:
+        pipe._resident[0] = _Resident(batch, {b: i for i, b in enumerate(ids)}, list(ids))
+        before = list(pipe._resident[0].ids)
+        for sel, chosen in ((AllBlocks(), ids), (None, ids), (RecentSinkBlocks(0, 10), ids), (FirstTwo(), [0, 1])):
+            out = pipe.decode(query, 0, sel)
+            expect, _ = O.attention(query.float().numpy(), pk, pv, sk, sv, valid, 4, 16, scale,
+                                    block_table=np.array(chosen, np.int32))
+            np.testing.assert_allclose(out.numpy(), expect, atol=2e-5, rtol=2e-5)
+        assert pipe._resident[0].ids == before
+    store.close()
