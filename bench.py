@@ -699,6 +699,9 @@ def main() -> int:
 
     import torch
 
+    import __graft_entry__
+
+    __graft_entry__.ensure_built()  # a fresh checkout: build once; otherwise load what is built
     from kvssd import _native
     from kvssd.backends import PackedBatch
     from kvssd.backends.hip import HipAttentionBackend

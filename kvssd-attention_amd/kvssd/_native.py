@@ -19,6 +19,7 @@ import torch  # noqa: F401  (must precede the library load; see module docstring
 # The in-tree build; KVSSD_HIP_LIBRARY names another build of the same ABI
 # (an instrumented one, say) for the whole process.
 LIB_PATH = Path(os.environ.get("KVSSD_HIP_LIBRARY") or Path(__file__).resolve().parent / "libkvssd_hip.so").resolve()
+LIB_PATH_OVERRIDDEN = bool(os.environ.get("KVSSD_HIP_LIBRARY"))
 ABI_VERSION = 5
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3

@@ -18,6 +18,14 @@ def pytest_configure(config: pytest.Config) -> None:
     config.addinivalue_line("markers", "gpu: needs a ROCm MI355X (gfx950) GPU; run with -m gpu")
 
 
+def pytest_sessionstart(session: pytest.Session) -> None:
+    # a fresh checkout has no built library: build it once (hipcc, gfx950);
+    # otherwise the tests load what is built
+    import __graft_entry__
+
+    __graft_entry__.ensure_built()
+
+
 def gpu_available() -> bool:
     import torch
 
