@@ -397,7 +397,8 @@ __global__ __launch_bounds__(64) void decode_mfma_kernel(const void* query, cons
   // padding ids of the last round (splits = ceil(units / blocks_per_split))
   if (u_begin >= p.units) return;
   const int u_end = min(p.units, u_begin + p.blocks_per_split);
-  // this workgroup's query heads: gqw heads from head0 (head0 + 4 quad ...)
+  // this workgroup's query heads: gqw heads from head0, i.e. query quads
+  // quad0 .. quad0 + QUADS - 1 of the kv head (the last one possibly partial)
   const int head0 = kvh * p.gq + 4 * quad0;
   const int gqw = min(p.gq - 4 * quad0, 4 * QUADS);
 
