@@ -84,6 +84,13 @@ typedef struct kvssd_decode_desc {
 /* ABI version of the loaded library (KVSSD_HIP_ABI_VERSION). */
 int kvssd_hip_abi_version(void);
 
+/* The build's identity: a hash of the HIP sources, this header and the
+ * compile flags the library was built from, as a NUL-terminated hex string
+ * (no counterpart in the reference, which JIT-builds its extension; the
+ * Python layer compares it with the tree's sources and refuses a stale
+ * build). */
+const char* kvssd_hip_build_id(void);
+
 /* 1 when `device` is a gfx950 GPU this library has code for, else 0, with the
  * reason written to `why` (NUL-terminated, at most why_len bytes).  Backs
  * HipAttentionBackend.probe(); replaces the device check of

@@ -218,6 +218,17 @@ extern "C" {
 
 __attribute__((visibility("default"))) int kvssd_hip_abi_version(void) { return KVSSD_HIP_ABI_VERSION; }
 
+// KVSSD_BUILD_ID comes from build.py (a hash of the sources and flags); the
+// marked copy lets a loader find it in the file without mapping the library
+#ifndef KVSSD_BUILD_ID
+#define KVSSD_BUILD_ID "unknown"
+#endif
+__attribute__((used)) static const char kBuildIdMarked[] = "kvssd-build-id:" KVSSD_BUILD_ID;
+
+__attribute__((visibility("default"))) const char* kvssd_hip_build_id(void) {
+  return kBuildIdMarked + sizeof("kvssd-build-id:") - 1;
+}
+
 __attribute__((visibility("default"))) const char* kvssd_hip_last_error(void) { return g_last_error.c_str(); }
 
 __attribute__((visibility("default"))) int kvssd_hip_device_ok(int device, char* why, size_t why_len) {

@@ -11,7 +11,9 @@ ctypes after ``import torch`` so it shares torch's HIP runtime
 from __future__ import annotations
 
 import argparse
+import hashlib
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -48,6 +50,37 @@ COMMON = [
 ]
 
 
+HEADER = HERE.parent.parent / "include" / "kvssd_hip.h"
+BUILD_ID_MARK = b"kvssd-build-id:"
+
+
+def source_hash() -> str:
+    """Hash of everything the library is built from: every HIP source and
+    header here, the public header and the compile flags (16 hex digits)."""
+    h = hashlib.sha256()
+    files = sorted(p for p in HERE.iterdir() if p.suffix in (".hip", ".hpp")) + [HEADER]
+    for f in files:
+        h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
+    h.update(" ".join(COMMON + SOURCES).encode())
+    return h.hexdigest()[:16]
+
+
+def built_id(path: Path = OUT) -> str | None:
+    """The build id stored in a built library (read from the file, without
+    loading it), or None when the file is absent or carries none."""
+    try:
+        data = path.read_bytes()
+    except OSError:
+        return None
+    m = re.search(re.escape(BUILD_ID_MARK) + rb"([0-9a-z]+)\0", data)
+    return m.group(1).decode() if m else None
+
+
+def is_stale(path: Path = OUT) -> bool:
+    """True when the library is absent or was built from other sources."""
+    return built_id(path) != source_hash()
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(path).exists():
@@ -75,7 +108,9 @@ def build(jobs: int = 0, verbose: bool = False, timeline: bool = False) -> Path:
     build_dir = BUILD / "timeline" if timeline else BUILD
     build_dir.mkdir(parents=True, exist_ok=True)
     cc = hipcc()
-    flags = [*COMMON, "-DKVSSD_TIMELINE"] if timeline else COMMON
+    flags = [*COMMON, f'-DKVSSD_BUILD_ID="{source_hash()}"']
+    if timeline:
+        flags.append("-DKVSSD_TIMELINE")
     objs = [build_dir / (Path(s).stem + ".o") for s in SOURCES]
     cmds = [[cc, *flags, "-c", str(HERE / s), "-o", str(o)] for s, o in zip(SOURCES, objs)]
     workers = jobs or min(len(cmds), os.cpu_count() or 1)

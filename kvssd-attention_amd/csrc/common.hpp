@@ -193,6 +193,54 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
+// --- V-scale exponent of a stage (the matrix-core kernels' fp16 W) ---
+//
+// The matrix-core kernels form W = p * scale_v in fp16 for the PV product.
+// p = 2^(s - m) <= 1, but scale_v spans fp16's whole range: W can overflow
+// (up to 65504 / 7 for INT4 scales, times a slot factor of up to 16) or fall
+// into fp16's subnormals (scale_v below ~6e-5: W loses its precision).  So
+// each stage (sub-block) takes e = E - 10, E the exponent of its largest
+// |scale_v| (|scale_v| < 2^(E+1)), and forms W = 2^(s - (m + e)) * scale_v:
+// every W is at most 2^11 (2^15 with the slot factor), and a token whose
+// weight 2^s * scale_v lies within 2^24 of the stage's largest possible one
+// stays a normal fp16 number.  The 2^-e rides on the softmax reference point:
+// the running (m, l, O) of a wave are all relative to m + e, so O / l is
+// unchanged, a stage whose m + e is larger rescales the state like a larger
+// max does, and lse = ln 2 (m + e + log2 l) as before.
+
+// Largest |x| over the four fp16 values of w, as fp16 bits (sign cleared,
+// so the integer order is the magnitude order; NaN and inf sort last).
+__device__ __forceinline__ uint32_t abs_max_bits(uint32_t w0, uint32_t w1) {
+  typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 m = __builtin_elementwise_max(__builtin_bit_cast(u16x2, w0 & 0x7FFF7FFFu),
+                                            __builtin_bit_cast(u16x2, w1 & 0x7FFF7FFFu));
+  const uint32_t lo = m[0], hi = m[1];
+  return lo > hi ? lo : hi;
+}
+
+// e = E - 10 for the largest of the wave's fp16 magnitude bits x (every lane
+// active; wave-uniform): DPP row rotations, then the four rows through
+// v_readlane.  s_nop 1 before each DPP read covers the VALU-write -> DPP-read
+// hazard (two wait states); nothing here involves the matrix core.  A zero or
+// subnormal maximum counts as 2^-14 (e = -24), inf and NaN as 2^16 (e = 6).
+__device__ __forceinline__ int wave_scale_exp(uint32_t x) {
+  uint32_t r;
+  asm("s_nop 1\n\t"
+      "v_max_u32_dpp %0, %1, %1 row_ror:8 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_ror:4 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_ror:2 row_mask:0xf bank_mask:0xf\n\t"
+      "s_nop 1\n\t"
+      "v_max_u32_dpp %0, %0, %0 row_ror:1 row_mask:0xf bank_mask:0xf"
+      : "=&v"(r)
+      : "v"(x));
+  const int ri = static_cast<int>(r);
+  const int a = max(max(__builtin_amdgcn_readlane(ri, 0), __builtin_amdgcn_readlane(ri, 16)),
+                    max(__builtin_amdgcn_readlane(ri, 32), __builtin_amdgcn_readlane(ri, 48)));
+  return max(a >> 10, 1) - 25;
+}
+
 // v from the lane of this lane's quad given by the DPP quad_perm control
 template <int kQuadPerm>
 __device__ __forceinline__ float quad_lane(float v) {

@@ -24,7 +24,9 @@
 //   Lane l ends with the 4 groups of head l/16, token l%16, and forms
 //   s = F * sm_scale * log2(e) * sum_g scale_k[t,g] * C[g] in registers.
 // softmax: exact per sub-block max (16-lane row reduction), running (m, l) in
-//   log2 units; p = 2^(s - m).
+//   log2 units; p = 2^(s - m), m including a per-sub-block power of two e set
+//   by the sub-block's largest V scale so that W below stays in fp16's normal
+//   range (common.hpp).
 // PV (v_mfma_f32_16x16x32_f16, per 32-token K step, 8 dim tiles, per quad):
 //   A = V^T codes as v: a 16x16 nibble transpose read (ds_read_b64_tr_b4) of
 //       the sub-block's V rows staged in LDS gives lane l one dim across 16
@@ -252,12 +254,21 @@ __device__ __forceinline__ void process(const Stage& st, const Cursor& c, uint8_
     }
   }
   // --------------------------------------------------------------- softmax
+  // the sub-block's V-scale exponent (wave-uniform; every lane row holds the
+  // same tokens): W = 2^(s - (m + e)) scale_v stays in fp16's normal range
+  uint32_t smax = 0u;
+#pragma unroll
+  for (int tau = 0; tau < kTiles; ++tau) {
+    const uint32_t b = abs_max_bits(st.sv[tau][0], st.sv[tau][1]);
+    smax = c.sb0 + 16 * tau + li < c.vb && b > smax ? b : smax;
+  }
+  const float e_v = static_cast<float>(wave_scale_exp(smax));
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
     float mx = score[quad][0];
 #pragma unroll
     for (int tau = 1; tau < kTiles; ++tau) mx = fmaxf(mx, score[quad][tau]);
-    mx = row_max16(mx);
+    mx = row_max16(mx) + e_v;  // the running reference: max of (sub-block max + e)
     const float m_new = fmaxf(qs[quad].m_run, mx);
     const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(qs[quad].m_run - m_new);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;

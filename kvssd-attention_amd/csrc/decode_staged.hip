@@ -46,7 +46,8 @@
 //   and forms s = sum_g scale_k[t, g] * C[g] with fp16-operand FMAs.
 // softmax: per-stage max by 16-lane DPP reduction, running (m, l) in log2
 //   units, p = 2^(s - m).  W[t, (h, g)] = p * scale_v[t, g] in fp16,
-//   written to LDS.
+//   written to LDS; m includes a per-stage power of two e set by the stage's
+//   largest V scale, which keeps W in fp16's normal range (common.hpp).
 // PV (v_mfma_f32_16x16x32_f16): A = W^T, rows (h, g); B = V codes from a
 //   16x16 nibble transpose read (ds_read_b64_tr_b4) of the staged V rows, one
 //   column per dim: one transpose read covers all 64 tokens of a wave's half
@@ -237,6 +238,10 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
     skw[tau] = *reinterpret_cast<const u32x2*>(buf + G::SK_OFF + sbyte);
     svw[tau] = *reinterpret_cast<const u32x2*>(buf + G::SV_OFF + sbyte);
   }
+  // the V scales of tile lq's token li: the lanes of the wave hold the
+  // stage's 64 tokens once each (for the stage's scale exponent)
+  u32x2 svm = *reinterpret_cast<const u32x2*>(
+      buf + G::SV_OFF + chunk_byte<G::SCPT>(kHalfTok * half + 16 * lq + li, w >> 1) + 8 * (w & 1));
   // transpose-read row of this lane: kk = li >> 3, row rho = li & 7,
   // slot s = 2(rho & 3) + (rho >> 2) -> token 16(s&3) + 4lq + 2kk + (s>>2)
   const int rho = li & 7;
@@ -320,7 +325,11 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
         svw[tau] = u32x2{0u, 0u};
       }
     }
+    if (16 * lq + li >= hv) svm = u32x2{0u, 0u};
   }
+  // the stage's V-scale exponent (wave-uniform): W = 2^(s - (m + e)) scale_v
+  // stays in fp16's normal range, whatever the range of the scales
+  const float e_v = static_cast<float>(wave_scale_exp(abs_max_bits(svm[0], svm[1])));
   // --------------------------------------------- V operands (no softmax dep)
   u32x4 va[NTR][2][NPAR];
   auto unpack_v = [&]() {
@@ -339,7 +348,8 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
   // --------------------------------------------------------------- softmax
 #pragma unroll
   for (int quad = 0; quad < QUADS; ++quad) {
-    const float mx = row_max16_of(score[quad][0], score[quad][1], score[quad][2], score[quad][3]);
+    // (the running reference is max over stages of the stage max plus e)
+    const float mx = row_max16_of(score[quad][0], score[quad][1], score[quad][2], score[quad][3]) + e_v;
     const float m_new = fmaxf(st.m_run[quad], mx);
     const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(st.m_run[quad] - m_new);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -348,8 +358,9 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
 #pragma unroll
     for (int tau = 0; tau < 4; ++tau) pr[tau] = __builtin_amdgcn_exp2f(score[quad][tau] - m_use);
     st.l_run[quad] = st.l_run[quad] * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-    // W = p * scale_v in fp16 (masked tokens: p = 0, scale 0); INT4 tiles
-    // 0, 1 sit in the K slots with F = 1024, so their W carries F/64 = 16.
+    // W = p * scale_v in fp16 (masked tokens: p = 0, scale 0), p relative to
+    // m + e so that W <= 2^11; INT4 tiles 0, 1 sit in the K slots with
+    // F = 1024, so their W carries F/64 = 16 (at most 2^15).
     // Each fp16 pair is one mixed-precision FMA into each half.
     uint32_t wlo[4], whi[4];  // per group g: (tile 0, tile 1), (tile 2, tile 3)
 #pragma unroll

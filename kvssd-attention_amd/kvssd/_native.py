@@ -10,6 +10,7 @@ the library.  Loading fails loudly; nothing falls back to another path.
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import os
 import threading
 from pathlib import Path
@@ -20,6 +21,8 @@ import torch  # noqa: F401  (must precede the library load; see module docstring
 # (an instrumented one, say) for the whole process.
 LIB_PATH = Path(os.environ.get("KVSSD_HIP_LIBRARY") or Path(__file__).resolve().parent / "libkvssd_hip.so").resolve()
 LIB_PATH_OVERRIDDEN = bool(os.environ.get("KVSSD_HIP_LIBRARY"))
+# the sources the in-tree build comes from (absent in an installed copy)
+BUILD_SCRIPT = Path(__file__).resolve().parent.parent / "csrc" / "build.py"
 ABI_VERSION = 5
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32, DTYPE_F64 = 0, 1, 2, 3
@@ -66,6 +69,7 @@ class RecordLayout(ctypes.Structure):
 _VP, _SZ, _I, _I64 = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int64
 SIGNATURES = {
     "kvssd_hip_abi_version": (_I, []),
+    "kvssd_hip_build_id": (ctypes.c_char_p, []),
     "kvssd_hip_device_ok": (_I, [_I, ctypes.c_char_p, _SZ]),
     "kvssd_hip_decode_workspace_bytes": (_I, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(_SZ)]),
     "kvssd_hip_decode_kernel": (_I, [ctypes.POINTER(DecodeDesc), ctypes.POINTER(_I)]),
@@ -97,6 +101,22 @@ class NativeError(RuntimeError):
 
 
 _loaded_from: Path | None = None
+
+
+def build_module():
+    """csrc/build.py as a module (source hash, build), or None without sources."""
+    if not BUILD_SCRIPT.exists():
+        return None
+    spec = importlib.util.spec_from_file_location("kvssd_hip_build", BUILD_SCRIPT)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def source_hash() -> str | None:
+    """Hash of the HIP sources next to the package (what a fresh build's id would be)."""
+    mod = build_module()
+    return None if mod is None else mod.source_hash()
 
 
 def load(path: str | Path | None = None) -> ctypes.CDLL:
@@ -132,8 +152,21 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
         if version != ABI_VERSION:
             _load_error = f"{want.name} ABI {version} != expected {ABI_VERSION}; rebuild it"
             raise RuntimeError(_load_error)
+        # the in-tree build must come from the sources beside it (a library
+        # named by KVSSD_HIP_LIBRARY is the caller's own)
+        if want == (Path(__file__).resolve().parent / "libkvssd_hip.so").resolve():
+            have, tree = lib.kvssd_hip_build_id().decode(), source_hash()
+            if tree is not None and have != tree:
+                _load_error = (f"{want.name} was built from other sources (build {have}, tree {tree}); "
+                               "rebuild it with python kvssd-attention_amd/csrc/build.py")
+                raise RuntimeError(_load_error)
         _lib, _loaded_from = lib, want
         return lib
+
+
+def build_id() -> str:
+    """The loaded library's build id (a hash of the sources it came from)."""
+    return load().kvssd_hip_build_id().decode()
 
 
 def available() -> tuple[bool, str]:

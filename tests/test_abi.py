@@ -28,6 +28,36 @@ def test_library_exports_every_declared_symbol():
     assert lib.kvssd_hip_abi_version() == _native.ABI_VERSION
 
 
+def test_build_id_matches_the_sources(tmp_path):
+    # the in-tree library carries the hash of the sources it was built from,
+    # both as an exported string and as a marked copy readable from the file
+    mod = _native.build_module()
+    assert mod is not None
+    tree = mod.source_hash()
+    assert _native.build_id() == tree == mod.built_id(_native.LIB_PATH)
+    assert not mod.is_stale()
+    # a library of other sources reads as stale (found without loading it)
+    data = _native.LIB_PATH.read_bytes()
+    other = tmp_path / "libother.so"
+    other.write_bytes(data.replace(b"kvssd-build-id:" + tree.encode(), b"kvssd-build-id:" + b"0" * len(tree)))
+    assert mod.built_id(other) == "0" * len(tree)
+    assert mod.is_stale(other) and mod.is_stale(tmp_path / "absent.so")
+
+
+def test_source_hash_covers_sources_header_and_flags(monkeypatch):
+    mod = _native.build_module()
+    base = mod.source_hash()
+    monkeypatch.setattr(mod, "COMMON", mod.COMMON + ["-DSOMETHING"])
+    assert mod.source_hash() != base
+    monkeypatch.undo()
+    header = mod.HEADER.read_bytes()
+    real = Path.read_bytes
+    monkeypatch.setattr(Path, "read_bytes", lambda p: real(p) + (b" " if p == mod.HEADER else b""))
+    assert mod.source_hash() != base
+    monkeypatch.undo()
+    assert mod.source_hash() == base and mod.HEADER.read_bytes() == header
+
+
 def test_argument_errors_are_negative_with_messages():
     lib = _native.load()
     desc = _native.DecodeDesc(32, 8, 128, 4, 128, 3, 32, 0, 0, 0, 0.1)
