@@ -233,6 +233,13 @@ int kvssd_hip_vllm_encode(const void* values, int dtype, int64_t elements, int b
 int kvssd_hip_vllm_decode(const uint8_t* payload, int64_t elements, int bits, int group_size, uint32_t crc, int dtype,
                           void* destination, int32_t* status, void* scratch, size_t scratch_bytes, void* stream);
 
+/* Plain streaming read of `bytes` bytes at `data` (16-byte aligned, a
+ * multiple of 16), XOR-folded into `sink` (at least 8,192 dwords).  A
+ * measurement helper with no counterpart in the reference: the HBM read rate
+ * a plain kernel attains on this GPU, which the decode's packed-KV rate is
+ * compared with. */
+int kvssd_hip_read_probe(const void* data, size_t bytes, uint32_t* sink, size_t sink_words, void* stream);
+
 /* hipMemcpyAsync host->device of `bytes` bytes on `stream`; `src` should be
  * page-locked for the copy to be asynchronous.  The staging copy of
  * KVSSDPipeline._stage (src/kvssd/pipeline.py:110-114). */

@@ -405,6 +405,16 @@ __attribute__((visibility("default"))) int kvssd_hip_vllm_decode(const uint8_t* 
                             scratch_bytes, static_cast<hipStream_t>(stream));
 }
 
+__attribute__((visibility("default"))) int kvssd_hip_read_probe(const void* data, size_t bytes, uint32_t* sink,
+                                                                size_t sink_words, void* stream) {
+  if (bytes % 16) return arg_error("read probe bytes must be a multiple of 16");
+  if (bytes > 0 && (!data || !sink)) return arg_error("a required buffer pointer is NULL");
+  if ((reinterpret_cast<uintptr_t>(data) % 16) != 0) return arg_error("read probe data must be 16-byte aligned");
+  if (sink_words < read_probe_sink_words())
+    return arg_error("read probe sink needs " + std::to_string(read_probe_sink_words()) + " words");
+  return launch_read_probe(data, bytes, sink, static_cast<hipStream_t>(stream));
+}
+
 __attribute__((visibility("default"))) int kvssd_hip_memcpy_h2d_async(void* dst, const void* src, size_t bytes,
                                                                       void* stream) {
   if (bytes == 0) return 0;

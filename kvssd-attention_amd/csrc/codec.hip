@@ -68,7 +68,49 @@ __global__ void dequantize_kernel(const uint8_t* __restrict__ packed, const uint
   out[i] = static_cast<float>(code - mid) * half_bits_to_float(scales[row * (head_dim / group_size) + dd / group_size]);
 }
 
+// Streaming read of n16 16-byte chunks: the plain HBM read rate a decode's
+// packed-KV traffic is measured against.  A workgroup reads contiguous
+// 32 KB pieces (eight 16-byte non-temporal loads in flight per thread, the
+// hint the decode kernels' code copies carry), the grid striding over the
+// buffer; the chunks fold by XOR and every wave leaves one dword in `sink`,
+// so no load can be elided.  (Measured on MI355X over 1 GiB: this shape
+// 7.0 TB/s; loads a whole grid apart 5.7 TB/s; without the hint 6.2 TB/s.)
+constexpr int kProbeThreads = 256;
+constexpr int kProbeBlocks = 2048;
+constexpr int kProbeUnroll = 8;
+typedef uint32_t probe_u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const probe_u32x4* __restrict__ p, int64_t n16,
+                                                                   uint32_t* __restrict__ sink) {
+  constexpr int64_t kPiece = kProbeThreads * kProbeUnroll;  // 16-byte chunks per workgroup pass
+  probe_u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kPiece; base < n16;
+       base += static_cast<int64_t>(gridDim.x) * kPiece) {
+    if (base + kPiece <= n16) {
+      probe_u32x4 v[kProbeUnroll];
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(p + base + u * kProbeThreads + threadIdx.x);
+#pragma unroll
+      for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u];
+    } else {
+      for (int64_t i = base + threadIdx.x; i < n16; i += kProbeThreads) acc ^= p[i];
+    }
+  }
+  uint32_t x = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  for (int m = 32; m > 0; m >>= 1) x ^= static_cast<uint32_t>(__shfl_xor(static_cast<int>(x), m, kWave));
+  if ((threadIdx.x & 63) == 0) sink[blockIdx.x * (kProbeThreads / kWave) + threadIdx.x / kWave] = x;
+}
+
 }  // namespace
+
+size_t read_probe_sink_words() { return static_cast<size_t>(kProbeBlocks) * (kProbeThreads / kWave); }
+
+int launch_read_probe(const void* data, size_t bytes, uint32_t* sink, hipStream_t stream) {
+  if (bytes == 0) return 0;
+  hipLaunchKernelGGL(read_probe_kernel, dim3(kProbeBlocks), dim3(kProbeThreads), 0, stream,
+                     static_cast<const probe_u32x4*>(data), static_cast<int64_t>(bytes / 16), sink);
+  return hip_status(hipGetLastError(), "read_probe launch");
+}
 
 int launch_unpack_codes(const uint8_t* packed, int bits, int64_t n_bytes, uint8_t* codes, hipStream_t stream) {
   if (n_bytes <= 0) return 0;

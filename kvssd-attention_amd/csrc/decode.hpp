@@ -96,6 +96,9 @@ int launch_vllm_decode(const uint8_t* payload, int64_t elements, int bits, int g
                        int dtype, void* destination, int32_t* status, void* scratch, size_t scratch_bytes,
                        hipStream_t stream);
 int launch_unpack_codes(const uint8_t* packed, int bits, int64_t n_bytes, uint8_t* codes, hipStream_t stream);
+// ---- measurement: a plain streaming read (codec.hip)
+size_t read_probe_sink_words();
+int launch_read_probe(const void* data, size_t bytes, uint32_t* sink, hipStream_t stream);
 int launch_dequantize(const uint8_t* packed, const uint16_t* scales, int64_t rows, int head_dim, int bits,
                       int group_size, float* out, hipStream_t stream);
 

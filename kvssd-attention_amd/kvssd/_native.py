@@ -88,6 +88,7 @@ SIGNATURES = {
     "kvssd_hip_vllm_encode": (_I, [_VP, _I, _I64, _I, _I, _VP, _VP, _VP, _SZ, _VP]),
     "kvssd_hip_vllm_decode": (_I, [_VP, _I64, _I, _I, ctypes.c_uint32, _I, _VP, _VP, _VP, _SZ, _VP]),
     "kvssd_hip_memcpy_h2d_async": (_I, [_VP, _VP, _SZ, _VP]),
+    "kvssd_hip_read_probe": (_I, [_VP, _SZ, _VP, _SZ, _VP]),
     "kvssd_hip_last_error": (ctypes.c_char_p, []),
 }
 

@@ -10,6 +10,7 @@ import torch
 from .backends import AttentionBackend, PackedBatch, resolve_attention_backend
 from .backends.reference import ReferenceAttentionBackend
 from .format import PackedKVBlock
+from .quant import dequantize_tensor
 
 # The fused native kernel here is the HIP one.  ``require_cuda_kernel=True`` in the
 # reference means "the fused native kernel must run"; on ROCm that kernel is
@@ -55,10 +56,32 @@ def packed_attention_reference(
     ``valid_tokens`` rows, the result is cast to the query's dtype."""
     if not blocks:
         raise ValueError("at least one block is required")
+    if not _uniform(blocks):
+        # blocks of different shapes or codecs: each dequantised on its own,
+        # their valid rows concatenated, as the reference does
+        keys = torch.cat([dequantize_tensor(b.key, torch.float32)[: b.valid_tokens] for b in blocks], dim=0)
+        values = torch.cat([dequantize_tensor(b.value, torch.float32)[: b.valid_tokens] for b in blocks], dim=0)
+        return reference_attention(query, keys.to(query.device), values.to(query.device), sm_scale)
     scale = 1.0 / math.sqrt(query.shape[-1]) if sm_scale is None else sm_scale
     batch = PackedBatch(*stack_blocks(blocks, query.device), blocks[0].key.bits, blocks[0].key.group_size)
     out, _ = ReferenceAttentionBackend().run(query, batch, scale)
     return out.to(query.dtype)
+
+
+def _fields(block: PackedKVBlock) -> tuple[torch.Tensor, ...]:
+    return (block.key.packed, block.value.packed, block.key.scales, block.value.scales)
+
+
+def _uniform(blocks: Sequence[PackedKVBlock]) -> bool:
+    """Whether every block has the first one's array shapes and dtypes and its codec."""
+    first = blocks[0]
+    sig = [(t.shape, t.dtype) for t in _fields(first)]
+    codec = (first.key.bits, first.key.group_size, first.value.bits, first.value.group_size)
+    return all(
+        [(t.shape, t.dtype) for t in _fields(b)] == sig
+        and (b.key.bits, b.key.group_size, b.value.bits, b.value.group_size) == codec
+        for b in blocks
+    )
 
 
 def stack_blocks(blocks: Sequence[PackedKVBlock], device: torch.device) -> tuple[torch.Tensor, ...]:
@@ -66,9 +89,20 @@ def stack_blocks(blocks: Sequence[PackedKVBlock], device: torch.device) -> tuple
     ``blocks`` on ``device`` (src/kvssd/attention.py:50-60).
 
     Each array is assembled once in host memory, block by block, and crosses
-    to the device in one copy; the valid counts follow as one int32 tensor."""
+    to the device in one copy; the valid counts follow as one int32 tensor.
+    Blocks whose arrays differ in shape or dtype from the first block's raise
+    RuntimeError, as the reference's ``torch.stack`` does (nothing is
+    broadcast)."""
     if not blocks:
         raise ValueError("at least one block is required")
+    sig = [(t.shape, t.dtype) for t in _fields(blocks[0])]
+    for i, block in enumerate(blocks):
+        got = [(t.shape, t.dtype) for t in _fields(block)]
+        if got != sig:
+            raise RuntimeError(
+                f"stack expects each tensor to be equal size and dtype, but got {got} at entry {i} "
+                f"and {sig} at entry 0"
+            )
     device = torch.device(device)
     fields = (
         lambda b: b.key.packed,

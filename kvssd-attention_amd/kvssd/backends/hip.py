@@ -27,6 +27,18 @@ from .base import BackendAvailability, PackedBatch
 _device_state: dict[int, tuple[bool, str]] = {}
 
 
+# The current stream's raw handle without building a Stream object (~0.2
+# against ~1.9 us per call): torch's generated bindings read it through this
+# private hook; where a torch build lacks it, the public Stream path serves.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def current_stream_handle(index: int) -> int:
+    if _RAW_STREAM is not None:
+        return int(_RAW_STREAM(index))
+    return int(torch.cuda.current_stream(index).cuda_stream)
+
+
 def _index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
@@ -263,10 +275,7 @@ class PreparedDecode:
         return self._launch(q)
 
     def _launch(self, q: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        # the current stream's raw handle, without building a Stream object
-        # (torch's own generated code reads it the same way; ~0.2 against
-        # ~1.9 us per call)
-        handle = torch._C._cuda_getCurrentRawStream(self._index)
+        handle = current_stream_handle(self._index)
         work = self._work.get(handle)
         if work is None:
             if len(self._work) >= self._MAX_STREAMS:

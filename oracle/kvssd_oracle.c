@@ -140,7 +140,7 @@ ORC_API void orc_pack_codes(const uint8_t* codes, int64_t n_codes, int bits, uin
   }
 }
 
-/* Inverse of orc_pack_codes: src/kvssd/quant.py:66-72. */
+/* Inverse of orc_pack_codes, as unpack_codes: src/kvssd/quant.py:40-46. */
 ORC_API void orc_unpack_codes(const uint8_t* packed, int64_t n_bytes, int bits, uint8_t* codes) {
   const int per = 8 / bits;
   for (int64_t b = 0; b < n_bytes; ++b)

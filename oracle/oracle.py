@@ -28,7 +28,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 LIB_PATH = HERE / "_build" / "libkvssd_oracle.so"
 
-# Record layout restated from src/kvssd/format.py:13-15 and :203-230.
+# Record layout restated from src/kvssd/format.py:14-16 (constants) and :104-131 (the encoder).
 ALIGNMENT = 4096
 MAGIC = b"KVSSD001"
 HEADER = struct.Struct("<8sIIIIIIIIIII")
@@ -124,7 +124,7 @@ def pack_np(codes: np.ndarray, bits: int) -> np.ndarray:
 
 
 def unpack_np(packed: np.ndarray, bits: int, elements: int | None = None) -> np.ndarray:
-    """Inverse of :func:`pack_np` (src/kvssd/quant.py:66-72)."""
+    """Inverse of :func:`pack_np`, as unpack_codes (src/kvssd/quant.py:40-46)."""
     per = 8 // bits
     shifts = np.arange(per, dtype=np.uint8) * bits
     vals = (packed[..., None] >> shifts) & ((1 << bits) - 1)

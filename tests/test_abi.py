@@ -77,6 +77,9 @@ def test_argument_errors_are_negative_with_messages():
     desc.group_size = 32
     assert lib.kvssd_hip_decode_workspace_bytes(ctypes.byref(desc), ctypes.byref(n)) == 0 and n.value > 0
     assert lib.kvssd_hip_unpack_codes(None, 3, 4, None, None) < 0
+    assert lib.kvssd_hip_read_probe(None, 17, None, 8192, None) < 0 and "multiple of 16" in _native.last_error()
+    assert lib.kvssd_hip_read_probe(16, 32, 16, 100, None) < 0 and "8192" in _native.last_error()
+    assert lib.kvssd_hip_read_probe(8, 32, 16, 8192, None) < 0 and "aligned" in _native.last_error()
     assert lib.kvssd_hip_merge_chunks(0, 8, None, None, None, None, None) < 0
 
 

@@ -20,7 +20,7 @@ from kvssd.attention import (
 )
 from kvssd.backends import PackedBatch
 from kvssd.backends.reference import ReferenceAttentionBackend
-from kvssd.format import CacheSpec
+from kvssd.format import CacheSpec, PackedKVBlock
 from kvssd.quant import quantize_tensor
 from kvssd.store import KVCacheStore
 from oracle import oracle as O
@@ -100,6 +100,46 @@ def test_stack_blocks_keeps_block_order_and_counts(tmp_path: Path):
     with pytest.raises(ValueError, match="at least one block"):
         stack_blocks([], torch.device("cpu"))
     store.close()
+
+
+def _block(tokens: int, bits: int, valid: int, seed: int) -> PackedKVBlock:
+    g = torch.Generator().manual_seed(seed)
+    k = torch.randn(tokens, 2, 32, generator=g, dtype=torch.float16)
+    v = torch.randn(tokens, 2, 32, generator=g, dtype=torch.float16)
+    return PackedKVBlock(0, seed, valid, quantize_tensor(k, bits, 8), quantize_tensor(v, bits, 8))
+
+
+def test_stack_blocks_rejects_blocks_unlike_the_first():
+    # the reference's torch.stack raises on a shape mismatch; a broadcastable
+    # block (1 token against 8) must not be replicated into the batch
+    with pytest.raises(RuntimeError, match="equal size"):
+        stack_blocks([_block(8, 4, 8, 1), _block(1, 4, 1, 2)], torch.device("cpu"))
+    with pytest.raises(RuntimeError, match="equal size"):
+        stack_blocks([_block(8, 4, 8, 1), _block(8, 2, 8, 2)], torch.device("cpu"))
+
+
+def test_packed_attention_reference_over_unlike_blocks():
+    # blocks of different lengths and bit widths: each is dequantised on its
+    # own and its valid rows concatenated (src/kvssd/attention.py:34-47);
+    # checked against float64 attention over the oracle's dequantisation
+    blocks = [_block(8, 4, 6, 1), _block(16, 2, 16, 2), _block(4, 4, 3, 3)]
+    q = torch.randn(4, 32, generator=torch.Generator().manual_seed(9), dtype=torch.float16)
+    out = packed_attention_reference(q, blocks, 0.2)
+    ks, vs = [], []
+    for b in blocks:
+        for t, dst in ((b.key, ks), (b.value, vs)):
+            codes = O.unpack_np(t.packed.numpy(), t.bits, t.original_shape[-1])
+            deq = O.dequantize_np(codes, t.scales.numpy(), t.bits, t.group_size)
+            dst.append(deq.reshape(t.original_shape)[: b.valid_tokens].astype(np.float64))
+    k, v = np.concatenate(ks), np.concatenate(vs)
+    qf = q.double().numpy()
+    want = np.zeros((4, 32))
+    for h in range(4):
+        s = 0.2 * (k[:, h // 2] @ qf[h])
+        p = np.exp(s - s.max())
+        want[h] = (p / p.sum()) @ v[:, h // 2]
+    assert out.dtype == torch.float16
+    np.testing.assert_allclose(out.float().numpy(), want, atol=2e-3, rtol=1e-2)
 
 
 @pytest.mark.parametrize("cuts", [(1,), (2, 5), (1, 2, 3, 4, 5, 6)])

@@ -32,8 +32,10 @@ def test_help_names_the_workloads_and_the_warmup_and_settle_defaults():
 
 
 def test_cpu_baseline_checks_the_timed_step_on_cpu_tensors():
-    """cpu_baseline's checks run on the host: fed the CPU reference's own result
-    as the timed step it reports ok; a perturbed one is not ok."""
+    """cpu_baseline's checks run on the host, against the oracle: fed the torch
+    reference backend's result as the timed step it reports ok; a perturbed
+    one, an all-zero output and one 10 % short (both within max-abs 2e-3 at
+    this output's size) are not ok."""
     import importlib.util
 
     import torch
@@ -52,7 +54,16 @@ def test_cpu_baseline_checks_the_timed_step_on_cpu_tensors():
         return out, lse
 
     good = bench.cpu_baseline(torch, query, cache, valid, 4, None, budget_s=1.0, gpu_run=gpu_run, timed=(out, lse))
+    assert good["kind"] == "port" and good["cores"] >= 1
     assert good["gpu_check"]["ok"] and good["timed_step_check"]["ok"] is True
-    assert good["timed_step_check"]["max_abs_out"] == 0.0
+    assert good["timed_step_check"]["max_abs_out"] < 1e-5 and good["torch_reference"]["ms_per_full_step"] > 0
     bad = bench.cpu_baseline(torch, query, cache, valid, 4, None, budget_s=1.0, timed=(out + 0.1, lse))
     assert bad["timed_step_check"]["ok"] is False and "gpu_check" not in bad
+    # outputs far below 2e-3 in magnitude: only the norm-relative check sees these
+    small = out * 1e-3
+    ref = bench.parity(small.numpy(), lse.numpy(), small.numpy(), lse.numpy())
+    assert ref["ok"]
+    assert not bench.parity(torch.zeros_like(small).numpy(), lse.numpy(), small.numpy(), lse.numpy())["ok"]
+    assert not bench.parity((0.9 * small).numpy(), lse.numpy(), small.numpy(), lse.numpy())["ok"]
+    # an lse shifted by 0.105 (a tenth of the tokens dropped) passes rtol 1e-2 at lse ~ 12, not max-abs 2e-3
+    assert not bench.parity(out.numpy(), (lse + 0.105).numpy(), out.numpy(), lse.numpy())["ok"]
