@@ -210,9 +210,18 @@ class PreparedDecode:
     The split partials go to a workspace kept per stream: calls on one stream
     are ordered, so each reuses it; calls on another stream get their own.
     The object holds references to the batch arrays (and block table), so
-    the pointers it passes stay valid while it lives."""
+    the pointers it passes stay valid while it lives.
+
+    Every call returns a fresh (out, lse) pair, as ``run`` does, but not from
+    two allocations: per stream the object allocates blocks of ``_ROWS``
+    outputs at once (on that stream, so torch's allocator orders their reuse
+    as it would a single tensor's) and hands out the next row of the current
+    block, whose views were made with the block.  A returned tensor is a
+    contiguous row of its block and keeps the block's storage alive (64 rows
+    of [QH, D] plus [QH]); two calls never share a row."""
 
     _MAX_STREAMS = 8
+    _ROWS = 64
 
     def __init__(self, backend: HipAttentionBackend, query, batch, sm_scale, block_table, out_dtype):
         if out_dtype is not None and out_dtype not in (torch.float32, query.dtype):
@@ -261,9 +270,12 @@ class PreparedDecode:
         self._out_shape = (query.shape[0], query.shape[1])
         self._out_dtype = query.dtype if typed else torch.float32
         self._work: dict[int, torch.Tensor] = {}
+        # per stream: [row views of out, row views of lse, next row]
+        self._rows: dict[int, list] = {}
+        self._sig = (torch.Size(self._qshape), self._qdtype, self._device)
 
     def __call__(self, query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        if tuple(query.shape) != self._qshape or query.dtype != self._qdtype or query.device != self._device:
+        if (query.shape, query.dtype, query.device) != self._sig:
             raise ValueError(
                 f"query {tuple(query.shape)} {query.dtype} on {query.device} does not match the prepared decode "
                 f"({self._qshape} {self._qdtype} on {self._device})"
@@ -282,8 +294,17 @@ class PreparedDecode:
                 self._work.pop(next(iter(self._work)))
             work = torch.empty((max(self._need, 1),), dtype=torch.uint8, device=self._device)
             self._work[handle] = work
-        out = torch.empty(self._out_shape, dtype=self._out_dtype, device=self._device)
-        lse = torch.empty((self._out_shape[0],), dtype=torch.float32, device=self._device)
+        rows = self._rows.get(handle)
+        if rows is None or rows[2] == self._ROWS:
+            if rows is None and len(self._rows) >= self._MAX_STREAMS:
+                self._rows.pop(next(iter(self._rows)))
+            outs = torch.empty((self._ROWS, *self._out_shape), dtype=self._out_dtype, device=self._device)
+            lses = torch.empty((self._ROWS, self._out_shape[0]), dtype=torch.float32, device=self._device)
+            rows = [outs.unbind(0), lses.unbind(0), 0]
+            self._rows[handle] = rows
+        i = rows[2]
+        rows[2] = i + 1
+        out, lse = rows[0][i], rows[1][i]
         rc = self._fn(
             self._desc_ref, q.data_ptr(), *self._ptrs, out.data_ptr(), lse.data_ptr(), work.data_ptr(), work.numel(),
             handle,

@@ -75,6 +75,8 @@ class KVSSDPipeline:
         self.stage_blocks = stage_blocks
         self.require_cuda_kernel = require_cuda_kernel
         self.attention_backend = resolve_required(require_cuda_kernel, attention_backend, self.device)
+        # resident decodes through the HIP backend's prepared decodes
+        self._hip = getattr(self.attention_backend, "name", None) == "hip"
         gpu = self.device.type == "cuda"
         self.transfer_stream = torch.cuda.Stream(device=self.device) if gpu else None
         # a second copy stream: successive chunks alternate between the two
@@ -173,15 +175,15 @@ class KVSSDPipeline:
 
     def _decode_resident(self, query: torch.Tensor, layer: int, selected: list[int]) -> torch.Tensor:
         res = self._resident[layer]
-        scale = 1.0 / math.sqrt(query.shape[-1])
-        run = self.attention_backend.run
-        if getattr(self.attention_backend, "name", None) == "hip":
-            # checks, descriptor and pointers once per (selection, query shape);
-            # the merge writes the query's dtype itself (no separate cast)
+        if self._hip:
+            # checks, descriptor and pointers once per (selection, query shape
+            # and dtype; the scale follows from the shape); the merge writes
+            # the query's dtype itself (no separate cast)
             table = self._table(res, selected)
-            key = (None if table is None else table.data_ptr(), tuple(query.shape), query.dtype, scale)
+            key = (None if table is None else table.data_ptr(), query.shape, query.dtype)
             prepared = res.prepared.get(key)
             if prepared is None:
+                scale = 1.0 / math.sqrt(query.shape[-1])
                 prepared = self.attention_backend.prepare(query, res.batch, scale, block_table=table, out_dtype=query.dtype)
                 if len(res.prepared) >= 2 * _TABLE_CACHE:
                     res.prepared.pop(next(iter(res.prepared)))
@@ -189,6 +191,8 @@ class KVSSDPipeline:
             out, _ = prepared(query)
             return out
         else:
+            scale = 1.0 / math.sqrt(query.shape[-1])
+            run = self.attention_backend.run
             rows = [res.row_of[b] for b in selected]
             idx = torch.tensor(rows, dtype=torch.long, device=self.device)
             b = res.batch
@@ -205,19 +209,20 @@ class KVSSDPipeline:
         layer: int,
         selector: BlockSelector | None = None,
     ) -> torch.Tensor:
-        selector = selector or AllBlocks()
         res = self._resident.get(layer)
-        if res is not None and type(selector) is AllBlocks:
+        if res is not None and (selector is None or type(selector) is AllBlocks):
             # every block of an HBM-resident layer, in the store's order: its
             # batch's row order (a store's block lists never change), with no
             # copy or compare of the id list on the per-call path
-            selected = res.ids
-        else:
-            selected = selector.select(self.store.blocks_for_layer(layer))
+            if res.ids:
+                return self._decode_resident(query.to(self.device), layer, res.ids)
+            raise ValueError("selector returned no blocks")
+        selector = selector or AllBlocks()
+        selected = selector.select(self.store.blocks_for_layer(layer))
         if not selected:
             raise ValueError("selector returned no blocks")
         query = query.to(self.device)
-        if layer in self._resident:
+        if res is not None:
             return self._decode_resident(query, layer, selected)
         if self.device.type == "cuda" and (layer in self._host or self.attention_backend.probe(self.device).accelerated):
             return self._decode_streamed(query, layer, selected)
