@@ -147,8 +147,9 @@ def pipeline_leg(torch, dev, tokens: int, bits: int, qh: int, sel, steps: int, w
     The public Python path, host work included (selection, argument checks,
     output allocation; the merge stores the fp16 output): a KVCacheStore of ``layers`` layers of
     the workload's shape is written to a temporary directory, every layer is
-    made resident, and the steps cycle through the layers (together larger
-    than the Infinity Cache) as a decode over a model's layers does."""
+    made resident, and the steps cycle through the layers as a decode over a
+    model's layers does (at 128K tokens the 4 layers, 604 MB, are larger than
+    the Infinity Cache; at 4K they fit in it)."""
     import tempfile
 
     from kvssd import KVCacheStore, KVSSDPipeline
@@ -911,16 +912,31 @@ def decode_workload(torch, dev, workload: str, steps: int, warmup: int, settle_m
             work.data_ptr(), work.numel(), sh,
         )
 
-    def step(i: int):
-        # one decode through the entry point the backend and the stager call
-        b = batches[i % copies]
-        rc = lib.kvssd_hip_fused_decode(
-            ctypes.byref(desc), query.data_ptr(), b.packed_k.data_ptr(), b.packed_v.data_ptr(),
-            b.scales_k.data_ptr(), b.scales_v.data_ptr(), b.valid_tokens.data_ptr(), tab_ptr,
-            out.data_ptr(), lse.data_ptr(), work.data_ptr(), work.numel(), sh,
-        )
-        if rc:
-            _native.check(rc, "decode")
+    # one decode through the entry point the backend and the stager call,
+    # with every pointer read once (and, where the CPython fast-call module is
+    # built, without ctypes' per-argument conversions: the host enqueue must
+    # stay well below a 4K step's GPU time)
+    arrays = [(b.packed_k.data_ptr(), b.packed_v.data_ptr(), b.scales_k.data_ptr(), b.scales_v.data_ptr(),
+               b.valid_tokens.data_ptr()) for b in batches]
+    tail = (tab_ptr, out.data_ptr(), lse.data_ptr(), work.data_ptr(), work.numel(), sh)
+    qptr = query.data_ptr()
+    fast = _native.fused_decode_fast()
+
+    if fast is not None:
+        fcall, fentry = fast
+        daddr = ctypes.addressof(desc)  # desc lives as long as this function's closures
+
+        def step(i: int):
+            rc = fcall(fentry, daddr, qptr, *arrays[i % copies], *tail)
+            if rc:
+                _native.check(rc, "decode")
+    else:
+        dref = ctypes.byref(desc)
+
+        def step(i: int):
+            rc = lib.kvssd_hip_fused_decode(dref, qptr, *arrays[i % copies], *tail)
+            if rc:
+                _native.check(rc, "decode")
 
     # clock settle (disclosed in the line): back-to-back decode steps for
     # settle_ms of wall time before the warm-up steps, so that the timed
@@ -1028,6 +1044,7 @@ def decode_workload(torch, dev, workload: str, steps: int, warmup: int, settle_m
         },
         "host_wall_ms_per_step": round(wall / steps * 1e3, 4),
         "host_enqueue_us_per_step": round(enqueue_us, 2),
+        "host_call": "kvssd_hip_fused_decode via " + ("the CPython fast-call module" if fast is not None else "ctypes"),
         "settle": {"ms": settle_ms, "steps": settle_steps,
                    "what": "untimed back-to-back decode steps before the W warm-up steps"},
         "finite": ok,
@@ -1048,8 +1065,11 @@ def other_workloads(torch, dev, args) -> dict:
     each timed step's output checked against the oracle."""
     rec = {}
     threads = min(os.cpu_count() or 1, 64)
+    # at least 200 timed steps each (a few ms of GPU time), whatever K the
+    # main line was asked for: 20 steps of a 23 us decode read ~5 % high
+    steps, warmup = max(args.steps, 200), max(args.warmup, 20)
     for w in OTHER_WORKLOADS:
-        line, ctx = decode_workload(torch, dev, w, args.steps, args.warmup, min(args.settle_ms, 20.0), args.kernel)
+        line, ctx = decode_workload(torch, dev, w, steps, warmup, min(args.settle_ms, 20.0), args.kernel)
         batch, bits = ctx["batch"], ctx["bits"]
         arr = {k: getattr(batch, n).cpu().numpy() for k, n in
                (("pk", "packed_k"), ("pv", "packed_v"), ("sk", "scales_k"), ("sv", "scales_v"))}
@@ -1058,6 +1078,7 @@ def other_workloads(torch, dev, args) -> dict:
                                       bits, ids, threads)
         t_out, t_lse = (x.cpu().numpy() for x in ctx["timed"])
         rec[w] = {
+            "steps": steps,
             "us_per_step": line["us_per_step"],
             "kernel_us": line["kernel_us"]["avg"],
             "roofline_frac": line["roofline"]["frac"],

@@ -5,7 +5,9 @@
 Each .hip file compiles to an object in csrc/_build/, then the objects link into
 kvssd-attention_amd/kvssd/libkvssd_hip.so, which the kvssd package loads with
 ctypes after ``import torch`` so it shares torch's HIP runtime
-(libamdhip64.so.7).
+(libamdhip64.so.7).  fastcall.c (a CPython module that calls one entry point
+of that library without ctypes' per-argument conversions) compiles with the
+host C compiler into kvssd/_fastcall<EXT_SUFFIX>.
 """
 
 from __future__ import annotations
@@ -17,6 +19,7 @@ import re
 import shutil
 import subprocess
 import sys
+import sysconfig
 from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
@@ -24,6 +27,8 @@ HERE = Path(__file__).resolve().parent
 PKG = HERE.parent / "kvssd"
 OUT = PKG / "libkvssd_hip.so"
 TIMELINE_OUT = PKG / "libkvssd_hip_timeline.so"
+FASTCALL_SRC = HERE / "fastcall.c"
+FASTCALL_OUT = PKG / ("_fastcall" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 BUILD = HERE / "_build"
 SOURCES = ["abi.hip", "decode_general.hip", "decode_mfma.hip", "decode_staged.hip", "merge.hip", "codec.hip", "records.hip", "vllm_codec.hip"]
 ARCH = "gfx950"
@@ -56,9 +61,10 @@ BUILD_ID_MARK = b"kvssd-build-id:"
 
 def source_hash() -> str:
     """Hash of everything the library is built from: every HIP source and
-    header here, the public header and the compile flags (16 hex digits)."""
+    header here, the CPython module's source, the public header and the
+    compile flags (16 hex digits)."""
     h = hashlib.sha256()
-    files = sorted(p for p in HERE.iterdir() if p.suffix in (".hip", ".hpp")) + [HEADER]
+    files = sorted(p for p in HERE.iterdir() if p.suffix in (".hip", ".hpp", ".c")) + [HEADER]
     for f in files:
         h.update(f.name.encode() + b"\0" + f.read_bytes() + b"\0")
     h.update(" ".join(COMMON + SOURCES).encode())
@@ -77,8 +83,9 @@ def built_id(path: Path = OUT) -> str | None:
 
 
 def is_stale(path: Path = OUT) -> bool:
-    """True when the library is absent or was built from other sources."""
-    return built_id(path) != source_hash()
+    """True when the library is absent or was built from other sources (or,
+    for the in-tree library, the CPython module built with it is absent)."""
+    return built_id(path) != source_hash() or (path == OUT and not FASTCALL_OUT.exists())
 
 
 def hipcc() -> str:
@@ -98,6 +105,19 @@ def _run(cmd: list[str], verbose: bool) -> None:
         raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build_fastcall(verbose: bool = False) -> Path:
+    """The CPython module, with the host C compiler against this interpreter's headers."""
+    cc = os.environ.get("CC") or shutil.which("gcc") or shutil.which("cc")
+    if not cc:
+        raise RuntimeError("no host C compiler (gcc) found")
+    include = sysconfig.get_paths()["include"]
+    tmp = FASTCALL_OUT.with_name(FASTCALL_OUT.name + ".tmp")
+    _run([cc, "-O2", "-shared", "-fPIC", "-Wall", "-Werror", f"-I{include}", str(FASTCALL_SRC), "-o", str(tmp)],
+         verbose)
+    os.replace(tmp, FASTCALL_OUT)
+    return FASTCALL_OUT
 
 
 def build(jobs: int = 0, verbose: bool = False, timeline: bool = False) -> Path:
@@ -120,6 +140,8 @@ def build(jobs: int = 0, verbose: bool = False, timeline: bool = False) -> Path:
     tmp = out.with_suffix(".so.tmp")
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)], verbose)
     os.replace(tmp, out)
+    if not timeline:
+        build_fastcall(verbose)
     return out
 
 

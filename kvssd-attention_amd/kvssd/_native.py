@@ -165,6 +165,27 @@ def load(path: str | Path | None = None) -> ctypes.CDLL:
         return lib
 
 
+FASTCALL_SIGNATURE = "kvssd_hip_fused_decode/13"
+
+
+def fused_decode_fast():
+    """(call, entry) for calling the loaded library's kvssd_hip_fused_decode
+    through the CPython module built beside it (csrc/fastcall.c):
+    ``call(entry, desc, query, packed_k, packed_v, scales_k, scales_v,
+    valid_tokens, block_table, out, lse, workspace, workspace_bytes, stream)``
+    with every pointer an int (or None) and ``desc`` the address of a
+    DecodeDesc, returning the status.  None when that module is absent or of
+    another signature (callers then use the ctypes function)."""
+    lib = load()
+    try:
+        from . import _fastcall
+    except ImportError:
+        return None
+    if getattr(_fastcall, "SIGNATURE", None) != FASTCALL_SIGNATURE:
+        return None
+    return _fastcall.fused_decode, ctypes.cast(lib.kvssd_hip_fused_decode, ctypes.c_void_p).value
+
+
 def build_id() -> str:
     """The loaded library's build id (a hash of the sources it came from)."""
     return load().kvssd_hip_build_id().decode()

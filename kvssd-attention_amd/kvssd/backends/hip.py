@@ -39,6 +39,12 @@ def current_stream_handle(index: int) -> int:
     return int(torch.cuda.current_stream(index).cuda_stream)
 
 
+# The current device's index; the hook torch.cuda.current_device() ends in,
+# without its lazy-initialisation check (the device is initialised by the time
+# a prepared decode exists).
+_CURRENT_DEVICE = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+
+
 def _index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
@@ -262,53 +268,77 @@ class PreparedDecode:
         self._desc = desc
         self._desc_ref = ctypes.byref(desc)
         self._fn = lib.kvssd_hip_fused_decode
+        # the same entry point without ctypes' per-argument conversions
+        # (~1.5 us a call), when the CPython module built with the library is there
+        fast = _native.fused_decode_fast()
+        self._fast, self._entry = fast if fast is not None else (None, None)
+        self._desc_addr = ctypes.addressof(desc)
         self._ptrs = (_ptr(pk), _ptr(pv), _ptr(sk), _ptr(sv), _ptr(valid), _ptr(table))
         self._device = query.device
         self._index = _index(query.device)
         self._qshape = tuple(query.shape)
+        self._qsize = torch.Size(self._qshape)
         self._qdtype = query.dtype
         self._out_shape = (query.shape[0], query.shape[1])
         self._out_dtype = query.dtype if typed else torch.float32
-        self._work: dict[int, torch.Tensor] = {}
-        # per stream: [row views of out, row views of lse, next row]
-        self._rows: dict[int, list] = {}
-        self._sig = (torch.Size(self._qshape), self._qdtype, self._device)
+        # per stream: [workspace pointer, workspace bytes, out row pointers,
+        # lse row pointers, next row, out rows, lse rows, workspace]
+        self._slots: dict[int, list] = {}
+
+    def matches(self, query: torch.Tensor) -> bool:
+        """Whether ``query`` has the prepared shape and dtype and sits on the prepared device."""
+        return query.dtype is self._qdtype and query.shape == self._qsize and query.get_device() == self._index
 
     def __call__(self, query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        if (query.shape, query.dtype, query.device) != self._sig:
+        if not self.matches(query):
             raise ValueError(
                 f"query {tuple(query.shape)} {query.dtype} on {query.device} does not match the prepared decode "
                 f"({self._qshape} {self._qdtype} on {self._device})"
             )
+        return self._call(query)
+
+    def try_call(self, query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """``self(query)``, or None (nothing launched) when the query does not match."""
+        return self._call(query) if self.matches(query) else None
+
+    def _call(self, query: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         q = query if query.is_contiguous() else query.contiguous()
-        if torch.cuda.current_device() != self._index:
+        if _CURRENT_DEVICE() != self._index:
             with torch.cuda.device(self._index):
                 return self._launch(q)
         return self._launch(q)
 
+    def _slot(self, handle: int, old: list | None) -> list:
+        """A stream's workspace (kept) and a fresh block of output rows."""
+        if old is None:
+            if len(self._slots) >= self._MAX_STREAMS:
+                self._slots.pop(next(iter(self._slots)))
+            work = torch.empty((max(self._need, 1),), dtype=torch.uint8, device=self._device)
+        else:
+            work = old[7]
+        outs = torch.empty((self._ROWS, *self._out_shape), dtype=self._out_dtype, device=self._device).unbind(0)
+        lses = torch.empty((self._ROWS, self._out_shape[0]), dtype=torch.float32, device=self._device).unbind(0)
+        slot = [
+            work.data_ptr(), work.numel(), [t.data_ptr() for t in outs], [t.data_ptr() for t in lses], 0, outs, lses,
+            work,
+        ]
+        self._slots[handle] = slot
+        return slot
+
     def _launch(self, q: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         handle = current_stream_handle(self._index)
-        work = self._work.get(handle)
-        if work is None:
-            if len(self._work) >= self._MAX_STREAMS:
-                self._work.pop(next(iter(self._work)))
-            work = torch.empty((max(self._need, 1),), dtype=torch.uint8, device=self._device)
-            self._work[handle] = work
-        rows = self._rows.get(handle)
-        if rows is None or rows[2] == self._ROWS:
-            if rows is None and len(self._rows) >= self._MAX_STREAMS:
-                self._rows.pop(next(iter(self._rows)))
-            outs = torch.empty((self._ROWS, *self._out_shape), dtype=self._out_dtype, device=self._device)
-            lses = torch.empty((self._ROWS, self._out_shape[0]), dtype=torch.float32, device=self._device)
-            rows = [outs.unbind(0), lses.unbind(0), 0]
-            self._rows[handle] = rows
-        i = rows[2]
-        rows[2] = i + 1
-        out, lse = rows[0][i], rows[1][i]
-        rc = self._fn(
-            self._desc_ref, q.data_ptr(), *self._ptrs, out.data_ptr(), lse.data_ptr(), work.data_ptr(), work.numel(),
-            handle,
-        )
-        _native.check(rc, "kvssd_hip_fused_decode")
+        slot = self._slots.get(handle)
+        if slot is None or slot[4] == self._ROWS:
+            slot = self._slot(handle, slot)
+        i = slot[4]
+        slot[4] = i + 1
+        if self._fast is not None:
+            rc = self._fast(
+                self._entry, self._desc_addr, q.data_ptr(), *self._ptrs, slot[2][i], slot[3][i], slot[0], slot[1], handle
+            )
+        else:
+            rc = self._fn(self._desc_ref, q.data_ptr(), *self._ptrs, slot[2][i], slot[3][i], slot[0], slot[1], handle)
+        if rc:
+            _native.check(rc, "kvssd_hip_fused_decode")
         self._backend.last_kernel = self.kernel
-        return out, lse
+        return slot[5][i], slot[6][i]

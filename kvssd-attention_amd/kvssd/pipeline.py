@@ -47,6 +47,8 @@ class _Resident:
     tables: dict[tuple[int, ...], torch.Tensor] = field(default_factory=dict)
     # prepared HIP decodes: (table address or None, query shape, dtype, scale) -> PreparedDecode
     prepared: dict[tuple, object] = field(default_factory=dict)
+    # the prepared decode of the whole layer in row order last used (AllBlocks)
+    whole: object | None = None
 
 
 _TABLE_CACHE = 8  # selections whose device block tables a resident layer keeps
@@ -189,6 +191,8 @@ class KVSSDPipeline:
                     res.prepared.pop(next(iter(res.prepared)))
                 res.prepared[key] = prepared
             out, _ = prepared(query)
+            if table is None:
+                res.whole = prepared
             return out
         else:
             scale = 1.0 / math.sqrt(query.shape[-1])
@@ -213,7 +217,13 @@ class KVSSDPipeline:
         if res is not None and (selector is None or type(selector) is AllBlocks):
             # every block of an HBM-resident layer, in the store's order: its
             # batch's row order (a store's block lists never change), with no
-            # copy or compare of the id list on the per-call path
+            # copy or compare of the id list on the per-call path; a query of
+            # the shape, dtype and device of the last such call goes straight
+            # to that call's prepared decode
+            if res.whole is not None:
+                r = res.whole.try_call(query)
+                if r is not None:
+                    return r[0]
             if res.ids:
                 return self._decode_resident(query.to(self.device), layer, res.ids)
             raise ValueError("selector returned no blocks")

@@ -238,3 +238,38 @@ def test_auto_takes_the_matrix_core_kernel_for_small_decodes():
         assert lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(k)) == 0 and k.value == _native.KERNEL_MFMA
         desc.num_blocks = 65
         assert lib.kvssd_hip_decode_kernel(ctypes.byref(desc), ctypes.byref(k)) == 0 and k.value == _native.KERNEL_STAGED
+
+
+def test_fast_call_module_matches_the_ctypes_call():
+    # the CPython module built with the library calls the same entry point
+    # with the same argument positions: each vector below fails a different
+    # argument check (and at least two, so no mapping could reach a launch),
+    # and both routes report the same status and message
+    fast = _native.fused_decode_fast()
+    assert fast is not None, "the CPython fast-call module was not built beside the library"
+    call, entry = fast
+    lib = _native.load()
+    assert entry == ctypes.cast(lib.kvssd_hip_fused_decode, ctypes.c_void_p).value
+    fake = 256
+
+    def both(desc, query, table, out, lse, work, nbytes):
+        ptrs = [query, fake, fake, fake, fake, fake, table, out, lse, work]
+        rc_c = lib.kvssd_hip_fused_decode(ctypes.byref(desc), *ptrs[:9], ptrs[9], nbytes, None)
+        msg_c = _native.last_error()
+        rc_f = call(entry, ctypes.addressof(desc), *ptrs, nbytes, None)
+        msg_f = _native.last_error()
+        assert rc_c < 0 and (rc_f, msg_f) == (rc_c, msg_c)
+        return msg_f
+
+    desc = _native.DecodeDesc(32, 8, 128, 64, 128, 4, 32, 0, 0, 0, 0.1)
+    assert "a required buffer pointer is NULL" in both(desc, fake, None, None, fake, fake, 1)  # out
+    assert "a required buffer pointer is NULL" in both(desc, fake, None, fake, None, fake, 1)  # lse
+    need = _need(both(desc, None, None, fake, fake, fake, 1))  # workspace bytes
+    assert need > 1
+    assert "workspace too small" in both(desc, None, None, fake, fake, None, 1 << 30)  # workspace pointer
+    desc.num_selected = 5
+    assert "num_selected must be 0 when block_table is NULL" in both(desc, fake, None, fake, fake, fake, 1)
+    desc.num_selected = 0
+    assert "at least one block is required" in both(desc, None, fake, fake, fake, fake, 1)  # table
+    with pytest.raises(TypeError, match="14 arguments"):
+        call(entry, ctypes.addressof(desc))

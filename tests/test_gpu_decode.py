@@ -507,7 +507,9 @@ def test_prepared_decode_matches_run(cuda_device):
             out2, lse2 = prepared(query)
         torch.cuda.current_stream(cuda_device).wait_stream(side)
         assert torch.equal(out2, ref_out) and torch.equal(lse2, ref_lse)
-        assert len(prepared._work) == 2
+        assert len(prepared._slots) == 2
+        # the signature check without launching
+        assert prepared.try_call(query.float()) is None and prepared.try_call(query[:16]) is None
         typed = backend.prepare(query, batch, 0.1, block_table=table, out_dtype=torch.float16)
         out16, _ = typed(query)
         assert out16.dtype == torch.float16 and torch.equal(out16, ref_out.to(torch.float16))
