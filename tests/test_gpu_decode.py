@@ -487,6 +487,35 @@ def test_two_phase_entry_points_write_the_query_dtype(cuda_device):
     assert torch.equal(out, fused) and torch.equal(lse, fused_lse)
 
 
+def test_prepared_decode_fast_call_and_ctypes_agree(cuda_device):
+    """A prepared decode launches through the CPython fast-call module when it
+    is built and through the ctypes function otherwise: both call the same
+    entry point with the same arguments, so their outputs are bit-equal (and
+    match the oracle), for the staged and the matrix-core kernels, with and
+    without a block table, and more calls than one block of output rows."""
+    assert _native.fused_decode_fast() is not None, "the fast-call module is built with the library"
+    rng = np.random.default_rng(17)
+    # (INT2 with 4 query heads per kv head: the scores on the fp6 x fp4 core)
+    for bits, nb, qh, kvh in ((4, 40, 32, 8), (2, 24, 16, 4)):
+        q, pk, pv, sk, sv, valid = make_batch(18 + bits, qh, kvh, 128, nb, 128, bits, 32)
+        q = torch.from_numpy(q).to(torch.float16).float().numpy()  # the values the kernel sees
+        query, batch = to_device(cuda_device, q, pk, pv, sk, sv, valid, bits, 32, torch.float16)
+        for table in (None, [int(i) for i in rng.permutation(nb)[: nb // 2]]):
+            ref_out, ref_lse = O.attention(
+                q, pk, pv, sk, sv, valid, bits, 32, 0.1, block_table=None if table is None else np.array(table, np.int32)
+            )
+            for kernel in ("staged", "mfma"):
+                fast = HipAttentionBackend(kernel).prepare(query, batch, 0.1, block_table=table)
+                slow = HipAttentionBackend(kernel).prepare(query, batch, 0.1, block_table=table)
+                assert fast._fast is not None
+                slow._fast = None  # the ctypes route
+                outs = [fast(query) for _ in range(70)] + [slow(query) for _ in range(70)]
+                torch.cuda.synchronize()
+                for out, lse in outs[1:]:
+                    assert torch.equal(out, outs[0][0]) and torch.equal(lse, outs[0][1])
+                check(outs[0][0], outs[0][1], ref_out, ref_lse)
+
+
 def test_prepared_decode_matches_run(cuda_device):
     """HipAttentionBackend.prepare: repeated calls (one workspace per stream),
     a call on a second stream, the typed output and a block table give run's
