@@ -59,8 +59,6 @@
 //   slot s -> token 16*(s&3) + 4q + 2kk + (s>>2) of the half; QK tile tau,
 //   lane li -> token 16*tau + li.  W of QK lane li, tile tau lives in slot
 //   4*u + tau of its (h, g) row, u = 8((li>>1)&1) + 2(li>>2) + (li&1).
-#include <type_traits>
-
 #include "staged_ops.hpp"
 #include "timeline.hpp"
 
@@ -212,45 +210,9 @@ struct WaveState {
 // Every LDS read of the stage goes out first, the four tiles' QK chains are
 // interleaved and V is unpacked before the softmax, so the two waves of a
 // SIMD have independent work to fill each other's latencies.
-// INT2 QK, query parts P .. NP-1: every tile's chain per part
-template <int P, int NP, int QUADS>
-__device__ __forceinline__ void qk_parts(f32x4 (&cc)[QUADS][4], const QueryOps6<QUADS, NP>& qo, const i32x8 (&kb)[4]) {
-  if constexpr (P < NP) {
-#pragma unroll
-    for (int quad = 0; quad < QUADS; ++quad)
-#pragma unroll
-      for (int tau = 0; tau < 4; ++tau) cc[quad][tau] = mfma_f6f4<P>(qo.qa[quad][P], kb[tau], cc[quad][tau], qo.qs[quad][P >> 2]);
-    qk_parts<P + 1, NP, QUADS>(cc, qo, kb);
-  }
-}
-
-// INT2 scores with a one-part (fp16 / bf16) query of at most 4 heads per kv
-// head take the fp6 x fp4 QK (staged_ops.hpp); INT4, and INT2 with a
-// two-part (fp32 / fp64) query or two query quads, the fp16 operands (the
-// fp6 parts' registers spilled there).
-template <int BITS, int QUADS, int QSPLIT>
-constexpr bool kFp6 = BITS == 2 && QSPLIT == 1 && QUADS == 1;
-
-template <int BITS, int QUADS, int QSPLIT>
-using QueryOpsOf =
-    typename std::conditional<kFp6<BITS, QUADS, QSPLIT>, QueryOps6<QUADS, kParts>, QueryOps<QUADS, QSPLIT>>::type;
-
-template <int BITS, int QUADS, int QSPLIT, typename QT>
-__device__ __forceinline__ auto query_load(const void* query, int gq, int head0, int lane) {
-  if constexpr (kFp6<BITS, QUADS, QSPLIT>) return fp6_query_load<QUADS, QT>(query, gq, head0, lane);
-  else return coop_query_load<BITS, QUADS, QT>(query, gq, head0, lane);
-}
-
-template <int BITS, int QUADS, int QSPLIT, typename RAW>
-__device__ __forceinline__ void query_build(QueryOpsOf<BITS, QUADS, QSPLIT>& qo, const RAW& raw, float scale_log2,
-                                            int lane, uint8_t* scratch) {
-  if constexpr (kFp6<BITS, QUADS, QSPLIT>) fp6_query_build<QUADS, kParts>(qo, raw, scale_log2, lane);
-  else coop_query_build<BITS, QUADS, QSPLIT>(qo, raw, scale_log2, lane, scratch);
-}
-
 template <int BITS, int QUADS, int QSPLIT, int KG>
 __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase, int hv, int w, int half, int li,
-                                              int lq, const Masks& mk, const QueryOpsOf<BITS, QUADS, QSPLIT>& qo,
+                                              int lq, const Masks& mk, const QueryOps<QUADS, QSPLIT>& qo,
                                               const u32x4& offa, WaveState<BITS, QUADS>& st) {
   using G = Geo<BITS, KG>;
   constexpr int KW = BITS == 4 ? 4 : 2;   // K words per lane and tile
@@ -308,13 +270,7 @@ __device__ __forceinline__ void compute_stage(const uint8_t* buf, uint8_t* wbase
   for (int quad = 0; quad < QUADS; ++quad)
 #pragma unroll
     for (int tau = 0; tau < 4; ++tau) cc[quad][tau] = qo.qcorr[quad];
-  if constexpr (kFp6<BITS, QUADS, QSPLIT>) {
-    // each tile's 128 dims in one fp6 x fp4 instruction per query part
-    i32x8 kb[4];
-#pragma unroll
-    for (int tau = 0; tau < 4; ++tau) kb[tau] = k_fp4(kraw[tau][0], kraw[tau][1]);
-    qk_parts<0, kParts, QUADS>(cc, qo, kb);
-  } else if constexpr (kEarlyV) {
+  if constexpr (kEarlyV) {
     // the four tiles' chains interleaved, one K word position at a time
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -548,7 +504,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
                   : next_stage<kStage>(c, units, n_units);
   };
 
-  QueryOpsOf<BITS, QUADS, QSPLIT> qo;
+  QueryOps<QUADS, QSPLIT> qo;
   Cursor cur{-1, 0, 0, -kStage};
   Cursor nxt{-1, 0, 0, -kStage};
   bool have = false, have_n = false;
@@ -585,11 +541,8 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
     else __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     KVSSD_STAMP(kStampRowsLanded);
-    const auto qraw = query_load<BITS, QUADS, QSPLIT, QT>(qrows, p.gq, w * p.gq, lane);
-    // (the fp16 operands pass through LDS scratch in the second buffer; the
-    // fp6 parts are built from registers once stage 1 is on its way)
-    if constexpr (!kFp6<BITS, QUADS, QSPLIT>)
-      query_build<BITS, QUADS, QSPLIT>(qo, qraw, p.scale_log2, lane, lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
+    coop_query_build<BITS, QUADS, QSPLIT>(qo, coop_query_load<BITS, QUADS, QT>(qrows, p.gq, w * p.gq, lane),
+                                          p.scale_log2, lane, lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
     __syncthreads();  // query rows and scratch consumed: the second buffer is free
     Cursor c1{-1, 0, 0, 0};
     bool issued1 = false;
@@ -603,7 +556,6 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
       }
       if (issued1) issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>(G::STAGE), c1, kvh0, wave, cm);
     }
-    if constexpr (kFp6<BITS, QUADS, QSPLIT>) query_build<BITS, QUADS, QSPLIT>(qo, qraw, p.scale_log2, lane, nullptr);
     KVSSD_STAMP(kStampStage1Issued);
     // stage 0 and the valid counts landed (only stage 1 may still be in flight)
     if (issued1) __builtin_amdgcn_s_waitcnt(vmcnt_wait(kStageCopies));
@@ -637,7 +589,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
     }
     // the query loads go out next: they complete in issue order, right after
     // the first stage's copies, instead of a round trip after them
-    const auto qraw = query_load<BITS, QUADS, QSPLIT, QT>(p.query, p.gq, head0, lane);
+    const QueryRaw<QUADS> qraw = coop_query_load<BITS, QUADS, QT>(p.query, p.gq, head0, lane);
     // the split's (block id, clamped valid count) list, read once into LDS
     for (int i = threadIdx.x; i < n_units; i += kThreads) {
       const int blk = p.table ? p.table[u_begin + i] : u_begin + i;
@@ -652,7 +604,8 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
     }
     // query operands, through per-wave scratch in the second stage buffer (its
     // first copies go out after the loop's first barrier)
-    query_build<BITS, QUADS, QSPLIT>(qo, qraw, p.scale_log2, lane, lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
+    coop_query_build<BITS, QUADS, QSPLIT>(qo, qraw, p.scale_log2, lane,
+                                          lds + G::STAGE + wave * coop_scratch_bytes<QUADS>);
     nxt = cur;
     have_n = have && advance(nxt);
   }

@@ -404,162 +404,5 @@ __device__ __forceinline__ void coop_query(QueryOps<QUADS, QSPLIT>& qo, const vo
 }
 
 
-// ------------------------------------------ INT2 QK on the fp6 x fp4 core ---
-//
-// INT2 scores go through v_mfma_scale_f32_16x16x128_f8f6f4 with K codes as
-// fp4 (e2m1) and the query as NP block-scaled fp6 (e2m3) parts: an fp6 x fp4
-// 16x16x128 instruction costs what one fp16 16x16x32 does (measured on
-// MI355X: 16.5 against 16.4 cycles; an fp8 operand doubles it), so a tile's
-// 128 dims take NP = 3 instructions instead of four, and the codes need one
-// AND per eight of them instead of an AND-OR per two.
-//
-// Operand layout (checked against a host model on the GPU, exact): lane l
-// holds row / column l % 16 and K block l / 16 (32 K elements), element e at
-// bits [w e, w e + w) of its register tuple (w = 6 for fp6, 4 for fp4; fp6
-// fills 6 dwords, fp4 4); the lane's selected byte (opsel) of its scale
-// register is the e8m0 exponent of its 32 elements.
-//
-// K: lane (token li, block lq) reads the 32 codes of dims 32 lq .. 32 lq + 31
-// (two dwords x0, x1, code j of a dword at bits 2j).  The fp4 nibble 00cc is
-// c / 2 exactly, so x & 0x33333333 puts the even codes of a dword in nibble
-// order and (x >> 2) & 0x33333333 the odd ones: K element e holds dim
-// 32 lq + kdim2(e).
-typedef int i32x8 __attribute__((ext_vector_type(8)));
-
-__host__ __device__ constexpr int kdim2(int e) { return 16 * (e >> 4) + 2 * (e & 7) + ((e >> 3) & 1); }
-
-__device__ __forceinline__ i32x8 k_fp4(uint32_t x0, uint32_t x1) {
-  constexpr uint32_t M = 0x33333333u;
-  typedef int i32x4 __attribute__((ext_vector_type(4)));
-  const i32x4 b = {static_cast<int>(x0 & M), static_cast<int>((x0 >> 2) & M), static_cast<int>(x1 & M),
-                   static_cast<int>((x1 >> 2) & M)};
-  // dwords 4-7 of an fp4 operand are not read by the instruction
-  return __builtin_shufflevector(b, b, 0, 1, 2, 3, -1, -1, -1, -1);
-}
-
-// QK of one query part P: A = part P of the query (fp6, scale byte P & 3 of
-// `scale`), B = a tile of K codes (fp4, scale 1)
-template <int P>
-__device__ __forceinline__ f32x4 mfma_f6f4(const i32x8& a, const i32x8& b, f32x4 c, uint32_t scale) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 2 /* A: fp6 e2m3 */, 4 /* B: fp4 e2m1 */, P & 3,
-                                                          static_cast<int>(scale), 0, 127);
-}
-
-// Query parts (fp16 / bf16 queries; fp32 / fp64 ones keep the two-part fp16
-// operands, whose registers six fp6 parts would exceed).  Part p of a (head,
-// group) block holds the block's 32 values v at scale 2^(e0 - 4p), e0 chosen
-// so that the block's largest |v| lies in [2, 4) 2^e0: part 0 rounds v 2^-e0
-// to fp6, each later part rounds the remainder times 16, so three parts keep
-// every value to 2^-13 of the block's largest (fp16 holds 11 bits).
-constexpr int kParts = 3;
-
-template <int QUADS, int NP>
-struct QueryOps6 {
-  i32x8 qa[QUADS][NP];               // fp6 parts (dwords 6-7 unused)
-  uint32_t qs[QUADS][(NP + 3) / 4];  // e8m0 scale bytes of the parts
-  f32x4 qcorr[QUADS];
-  float kscale[QUADS];
-};
-
-template <int QUADS>
-struct QueryRaw32 {
-  float x[QUADS][32];  // dims 32 lq + kdim2(e) of this lane's query head, quad by quad
-};
-
-// Loads of the query values a lane's A operand needs (head quad * 4 + li / 4
-// of the kv head's gq heads from head0, its dim group lq), issued for every
-// lane (the head clamped into range) and masked afterwards: a load under a
-// lane condition compiles to a branch that waits for every outstanding
-// memory operation.
-template <int QUADS, typename QT>
-__device__ __forceinline__ QueryRaw32<QUADS> fp6_query_load(const void* query, int gq, int head0, int lane) {
-  const int li = lane & 15, lq = lane >> 4;
-  QueryRaw32<QUADS> r;
-#pragma unroll
-  for (int quad = 0; quad < QUADS; ++quad) {
-    const int hq = quad * 4 + (li >> 2);
-    const bool live = hq < gq && (li & 3) == lq;
-    const int base = (head0 + (hq < gq ? hq : 0)) * 128 + 32 * lq;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      const float v = load_query<QT>(query, base + kdim2(e));
-      r.x[quad][e] = live ? v : 0.0f;
-    }
-  }
-  return r;
-}
-
-// The parts come from the hardware conversions (v_cvt_scalef32_2xpk16_fp6_f32
-// and its inverse, checked on the GPU against a host encoder): the forward
-// conversion rounds v / s to nearest even and writes element 2i from its
-// first operand's element i, element 2i + 1 from its second's, in the MFMA
-// operand layout; the inverse returns code * s element by element.  Part p
-// converts the remainder of the parts before it at s = 16^-p, so each
-// remainder is one subtraction.  (A conversion whose destination overlaps a
-// source register that is no longer live returned wrong elements: every
-// source here stays live past its conversion, as the remainder needs it.)
-template <int QUADS, int NP>
-__device__ __forceinline__ void fp6_query_build(QueryOps6<QUADS, NP>& qo, const QueryRaw32<QUADS>& r,
-                                                float scale_log2, int lane) {
-  typedef float f32x16 __attribute__((ext_vector_type(16)));
-  const int lq = lane >> 4;
-#pragma unroll
-  for (int quad = 0; quad < QUADS; ++quad) {
-    float mx = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) mx = fmaxf(mx, fabsf(r.x[quad][e]));
-    int e0 = 0;
-    // blocks of non-finite values give NaN scores; blocks below 2^-113 count
-    // as zero (every part's scale must stay a normal e8m0 exponent)
-    const bool finite = isfinite(mx);
-    bool zero = !(mx > 0.0f) || !finite;
-    if (!zero) {
-      frexpf(mx, &e0);  // mx in [2^(e0-1), 2^e0)
-      e0 -= 2;          // mx 2^-e0 in [2, 4)
-      zero = e0 < -115;
-    }
-    // the remainder, split by operand: element 2i in lo[i], 2i + 1 in hi[i]
-    f32x16 lo, hi;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      lo[i] = zero ? 0.0f : ldexpf(r.x[quad][2 * i], -e0);
-      hi[i] = zero ? 0.0f : ldexpf(r.x[quad][2 * i + 1], -e0);
-    }
-    float held = 0.0f;  // the block's values as the parts hold them, summed (units 2^e0)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) held += lo[i] + hi[i];
-    uint32_t scales[(NP + 3) / 4] = {};
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const float s = 1.0f / static_cast<float>(1 << (4 * p));  // 16^-p, exact
-      const auto code = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(lo, hi, s);
-      const auto back = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(code, s);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        lo[i] -= back[2 * i];
-        hi[i] -= back[2 * i + 1];
-      }
-      qo.qa[quad][p] = i32x8{static_cast<int>(code[0]), static_cast<int>(code[1]), static_cast<int>(code[2]),
-                             static_cast<int>(code[3]), static_cast<int>(code[4]), static_cast<int>(code[5]), 0, 0};
-      // e8m0: 127 + exponent; 255 (NaN) for a block holding a non-finite value
-      const int ex = !finite ? 255 : zero ? 0 : 127 + e0 - 4 * p;
-      scales[p >> 2] |= static_cast<uint32_t>(ex) << (8 * (p & 3));
-    }
-#pragma unroll
-    for (int i = 0; i < (NP + 3) / 4; ++i) qo.qs[quad][i] = scales[i];
-    // minus what the parts leave out (this use keeps the last remainder, and
-    // so the last conversion's sources, live)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) held -= lo[i] + hi[i];
-    const float sum = zero ? 0.0f : ldexpf(held, e0);
-    // C init of QK lane (li, lq), register g: row (head lq, group g) starts
-    // at minus that block's sum, held by its live lane (4 lq + g, g)
-#pragma unroll
-    for (int g = 0; g < 4; ++g) qo.qcorr[quad][g] = -__shfl(sum, 4 * lq + g + 16 * g, kWave);
-    // C = sum q (c - 2) / 2 per group: the score carries the 2
-    qo.kscale[quad] = 2.0f * scale_log2;
-  }
-}
-
 }  // namespace
 }  // namespace kvssd

@@ -37,6 +37,7 @@ import torch
 
 import needles as N
 from kvssd.backends import PackedBatch
+from oracle import oracle as O
 from kvssd import records_hip
 from kvssd.backends.hip import HipAttentionBackend
 
@@ -158,3 +159,53 @@ def test_value_range_128k_tokens(cuda_device, base, keys_q, vscale, pattern):
         for kernel, (out, lse) in results.items():
             norm_rel = float(np.linalg.norm(out - c_out) / np.linalg.norm(c_out))
             assert norm_rel > 2 * N.NORM_RTOL, f"{what} {kernel}: the check would pass with one needle dropped"
+
+
+def large_score_case(bits: int, nb: int, mult: float, outliers: bool):
+    """Peaked attention with large scores: one needle token per kv head whose
+    key points along the sum of the head's query group; the query scaled by
+    ``mult`` (largest lse ~ 30-40 mult with outliers, ~ 7-8 mult without), with
+    one dim per 32-dim group 20 times the others when ``outliers``."""
+    rng = np.random.default_rng(9)
+    kvh, qh, d, bt = 8, 32, 128, 128
+    k = rng.standard_normal((nb * bt, kvh, d)).astype(np.float32)
+    v = rng.standard_normal((nb * bt, kvh, d)).astype(np.float32)
+    q0 = rng.standard_normal((qh, d)).astype(np.float32)
+    qs = q0.reshape(kvh, qh // kvh, d).sum(1)
+    needle = (nb * bt) // 3
+    k[needle] = qs / np.linalg.norm(qs, axis=1, keepdims=True) * math.sqrt(d)
+    pk, sk, _ = O.quantize_blocks(k, bits, 32, bt)
+    pv, sv, _ = O.quantize_blocks(v, bits, 32, bt)
+    q = q0 * np.float32(mult)
+    if outliers:
+        q[:, 5::32] *= 20
+    q16 = q.astype(np.float16)
+    return q16, [pk, pv, sk, sv], np.full(nb, bt, np.int32)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+@pytest.mark.parametrize("nb", [64, 256])
+def test_large_scores_and_query_outliers(cuda_device, bits, nb):
+    # The reference scores in fp32 (src/kvssd/backends/reference.py:42-45): a
+    # plain fp32 dot product and logsumexp stay within 1e-4 of float64 here
+    # even at lse ~ 1,300.  A kernel whose query operand kept only a fixed
+    # number of bits relative to a 32-dim block's largest value errs in
+    # proportion to the scores: three block-scaled fp6 parts missed lse by
+    # 2.5e-3 at lse ~ 29 with the outlier dims (64 blocks) and by 3.8e-3 at
+    # lse ~ 41 (256 blocks).  The cases stop at lse ~ 250: beyond that the
+    # staged INT2 scores, which remove the codes' offset through the fp32
+    # accumulator, round by more than 2e-3 in absolute terms (3.8e-3 at lse
+    # ~ 1,300, 2.9e-6 relative).  64 blocks take the staged kernel's 4-kv-head
+    # workgroups, 256 blocks its 8-kv-head ones.
+    scale = 1 / math.sqrt(128)
+    for mult, outliers in ((1.0, True), (4.0, True), (16.0, False), (32.0, False)):
+        q16, arrays, valid = large_score_case(bits, nb, mult, outliers)
+        qf = q16.astype(np.float32)
+        ref_out, ref_lse = O.attention(qf, *arrays, valid, bits, 32, scale)
+        batch = PackedBatch(*(torch.from_numpy(a).to(cuda_device) for a in arrays),
+                            torch.from_numpy(valid).to(cuda_device), bits, 32)
+        for kernel in KERNELS:
+            backend = HipAttentionBackend(kernel)
+            out, lse = backend.run(torch.from_numpy(q16).to(cuda_device), batch, scale)
+            what = f"INT{bits} {nb} blocks x{mult} outliers={outliers} {kernel} (lse up to {ref_lse.max():.0f})"
+            assert_range_match(out.cpu().numpy(), lse.cpu().numpy(), ref_out, ref_lse, what)
