@@ -59,6 +59,8 @@
 //   slot s -> token 16*(s&3) + 4q + 2kk + (s>>2) of the half; QK tile tau,
 //   lane li -> token 16*tau + li.  W of QK lane li, tile tau lives in slot
 //   4*u + tau of its (h, g) row, u = 8((li>>1)&1) + 2(li>>2) + (li&1).
+#include <type_traits>
+
 #include "staged_ops.hpp"
 #include "timeline.hpp"
 
@@ -431,6 +433,16 @@ __device__ __forceinline__ void wait_copies_left(int extra) {
   }
 }
 
+// INT2's stage round is bound by its VALU: with the stage loop unrolled by the
+// two stage buffers, every LDS address of a stage is a loop-invariant lane
+// offset plus a constant the LDS instructions take as their immediate offset
+// (a runtime buffer costs ~10 address adds per wave and stage): the INT2 128K
+// GQA-4 step 23.5-23.6 -> 23.25-23.3 us (two rounds of three A/B pairs, one
+// box each), GQA 8 unchanged.  INT4 measured no faster with it (128K +0.15 us)
+// and keeps the loop below; the two-quad fp32 / fp64 INT2 form would spill.
+template <int BITS, int QUADS, int QSPLIT>
+constexpr bool kUnrollByBuffer = BITS == 2 && !(QUADS == 2 && QSPLIT == 2);
+
 template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
 __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* query, const uint8_t* pk,
                                                                  const uint8_t* pv, const uint8_t* sk,
@@ -629,29 +641,58 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
   // ------------------------------------------- double-buffered stage loop
   // the stage after the current one is looked up a step ahead, so that its
   // copies go out right after the barrier
-  int buf = 0;
   bool first = true;
   [[maybe_unused]] int stage_no = 0;
   KVSSD_STAMP(kStampLoop);
-  while (have) {
-    if (!first || wait0) {
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
-      __syncthreads();                     // ... everyone's; and the other buffer is free
+  if constexpr (kUnrollByBuffer<BITS, QUADS, QSPLIT>) {
+    // one pass with the stage buffer B a compile-time constant
+    auto pass = [&](auto buffer) {
+      constexpr int B = decltype(buffer)::value;
+      if (!first || wait0) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
+        __syncthreads();                     // ... everyone's; and the other buffer is free
+      }
+      KVSSD_STAMP(kStampStage + min(stage_no++, 15));
+      if (have_n && !(first && pre1))
+        issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>((B ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
+      first = false;
+      const int hv = min(kStage, cur.vb - cur.sb0) - kHalfTok * half;
+      if (hv > 0) {
+        uint8_t* sbuf = lds + B * G::STAGE;
+        uint8_t* wbase = G::W_IN_K ? sbuf : lds + 2 * G::STAGE + wave * QUADS * 2048;
+        compute_stage<BITS, QUADS, QSPLIT, KG>(sbuf, wbase, hv, w, half, li, lq, mk, qo, offa, st);
+      }
+      cur = nxt;
+      have = have_n;
+      if (have) have_n = advance(nxt);
+    };
+    while (have) {
+      pass(std::integral_constant<int, 0>{});
+      if (!have) break;
+      pass(std::integral_constant<int, 1>{});
     }
-    KVSSD_STAMP(kStampStage + min(stage_no++, 15));
-    if (have_n && !(first && pre1))
-      issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>((buf ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
-    first = false;
-    const int hv = min(kStage, cur.vb - cur.sb0) - kHalfTok * half;
-    if (hv > 0) {
-      uint8_t* sbuf = lds + buf * G::STAGE;
-      uint8_t* wbase = G::W_IN_K ? sbuf : lds + 2 * G::STAGE + wave * QUADS * 2048;
-      compute_stage<BITS, QUADS, QSPLIT, KG>(sbuf, wbase, hv, w, half, li, lq, mk, qo, offa, st);
+  } else {
+    int buf = 0;
+    while (have) {
+      if (!first || wait0) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of the stage landed
+        __syncthreads();                     // ... everyone's; and the other buffer is free
+      }
+      KVSSD_STAMP(kStampStage + min(stage_no++, 15));
+      if (have_n && !(first && pre1))
+        issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>((buf ^ 1) * G::STAGE), nxt, kvh0, wave, cm);
+      first = false;
+      const int hv = min(kStage, cur.vb - cur.sb0) - kHalfTok * half;
+      if (hv > 0) {
+        uint8_t* sbuf = lds + buf * G::STAGE;
+        uint8_t* wbase = G::W_IN_K ? sbuf : lds + 2 * G::STAGE + wave * QUADS * 2048;
+        compute_stage<BITS, QUADS, QSPLIT, KG>(sbuf, wbase, hv, w, half, li, lq, mk, qo, offa, st);
+      }
+      cur = nxt;
+      have = have_n;
+      if (have) have_n = advance(nxt);
+      buf ^= 1;
     }
-    cur = nxt;
-    have = have_n;
-    if (have) have_n = advance(nxt);
-    buf ^= 1;
   }
 
   KVSSD_STAMP(kStampLoopEnd);
