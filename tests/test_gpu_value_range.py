@@ -209,3 +209,35 @@ def test_large_scores_and_query_outliers(cuda_device, bits, nb):
             out, lse = backend.run(torch.from_numpy(q16).to(cuda_device), batch, scale)
             what = f"INT{bits} {nb} blocks x{mult} outliers={outliers} {kernel} (lse up to {ref_lse.max():.0f})"
             assert_range_match(out.cpu().numpy(), lse.cpu().numpy(), ref_out, ref_lse, what)
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_unusual_softmax_scales(cuda_device, bits):
+    # sm_scale is any float the caller passes (src/kvssd/backends/reference.py:
+    # 42-45 multiplies the scores by it): zero (uniform weights, lse = ln of the
+    # token count, out = the mean of the values), tiny, larger than 1/sqrt(D)
+    # and negative, on every kernel, 64 blocks (the staged kernel's 4-kv-head
+    # workgroups) and 256 (its 8-kv-head ones)
+    rng = np.random.default_rng(3)
+    for nb in (64, 256):
+        k = rng.standard_normal((nb * 128, 8, 128)).astype(np.float32)
+        v = rng.standard_normal((nb * 128, 8, 128)).astype(np.float32)
+        pk, sk, _ = O.quantize_blocks(k, bits, 32, 128)
+        pv, sv, _ = O.quantize_blocks(v, bits, 32, 128)
+        valid = np.full(nb, 128, np.int32)
+        valid[nb // 2] = 77  # one partial block
+        q16 = rng.standard_normal((32, 128)).astype(np.float16)
+        batch = PackedBatch(*(torch.from_numpy(a).to(cuda_device) for a in (pk, pv, sk, sv, valid)), bits, 32)
+        for scale in (0.0, 1e-4, 0.5, 2.0, -0.1):
+            ref_out, ref_lse = O.attention(q16.astype(np.float32), pk, pv, sk, sv, valid, bits, 32, scale)
+            if scale == 0.0:
+                # the closed form the oracle must meet first
+                n = int(valid.sum())
+                assert np.allclose(ref_lse, math.log(n), atol=1e-6)
+                vals = O.dequantize_np(O.unpack_np(pv, bits), sv, bits, 32).reshape(nb, 128, 8, 128)
+                mean = np.concatenate([vals[b, : valid[b]] for b in range(nb)]).mean(0)  # [8, 128]
+                assert np.allclose(ref_out, np.repeat(mean, 4, axis=0), atol=1e-5)
+            for kernel in KERNELS:
+                out, lse = HipAttentionBackend(kernel).run(torch.from_numpy(q16).to(cuda_device), batch, scale)
+                what = f"INT{bits} {nb} blocks sm_scale {scale} {kernel} (lse up to {ref_lse.max():.0f})"
+                assert_range_match(out.cpu().numpy(), lse.cpu().numpy(), ref_out, ref_lse, what)
