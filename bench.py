@@ -1054,7 +1054,7 @@ def decode_workload(torch, dev, workload: str, steps: int, warmup: int, settle_m
     return line, ctx
 
 
-# the other BASELINE workloads, reported compactly beside the headline one
+# the other decode workloads (4K, INT2 128K, sparse 256K GQA 8), reported compactly beside the headline one
 OTHER_WORKLOADS = ("int4_gqa_4k", "int2_gqa_128k", "int4_gqa8_256k_sparse")
 
 
