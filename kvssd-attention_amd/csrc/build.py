@@ -84,8 +84,10 @@ def built_id(path: Path = OUT) -> str | None:
 
 def is_stale(path: Path = OUT) -> bool:
     """True when the library is absent or was built from other sources (or,
-    for the in-tree library, the CPython module built with it is absent)."""
-    return built_id(path) != source_hash() or (path == OUT and not FASTCALL_OUT.exists())
+    for the in-tree library, the CPython module built with it is absent or
+    was built from other sources)."""
+    tree = source_hash()
+    return built_id(path) != tree or (path == OUT and built_id(FASTCALL_OUT) != tree)
 
 
 def hipcc() -> str:
@@ -114,8 +116,8 @@ def build_fastcall(verbose: bool = False) -> Path:
         raise RuntimeError("no host C compiler (gcc) found")
     include = sysconfig.get_paths()["include"]
     tmp = FASTCALL_OUT.with_name(FASTCALL_OUT.name + ".tmp")
-    _run([cc, "-O2", "-shared", "-fPIC", "-Wall", "-Werror", f"-I{include}", str(FASTCALL_SRC), "-o", str(tmp)],
-         verbose)
+    _run([cc, "-O2", "-shared", "-fPIC", "-Wall", "-Werror", f'-DKVSSD_BUILD_ID="{source_hash()}"', f"-I{include}",
+          str(FASTCALL_SRC), "-o", str(tmp)], verbose)
     os.replace(tmp, FASTCALL_OUT)
     return FASTCALL_OUT
 

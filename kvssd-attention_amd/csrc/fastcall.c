@@ -22,6 +22,14 @@ typedef int (*fused_decode_fn)(const void*, const void*, const void*, const void
 
 enum { kArgs = 14, kBytesArg = 12 };
 
+/* The hash of the sources this module and the library were built from
+ * (build.py passes it to both); also kept as a marked string, so that the
+ * build script can read it from the file without importing the module. */
+#ifndef KVSSD_BUILD_ID
+#define KVSSD_BUILD_ID "unknown"
+#endif
+__attribute__((used)) static const char kBuildIdMarked[] = "kvssd-build-id:" KVSSD_BUILD_ID;
+
 static int as_pointer(PyObject* o, void** p) {
   if (o == Py_None) {
     *p = NULL;
@@ -67,7 +75,8 @@ static struct PyModuleDef module = {PyModuleDef_HEAD_INIT, "_fastcall", NULL, -1
 PyMODINIT_FUNC PyInit__fastcall(void) {
   PyObject* m = PyModule_Create(&module);
   /* the argument list above, for the loader's check */
-  if (m != NULL && PyModule_AddStringConstant(m, "SIGNATURE", "kvssd_hip_fused_decode/13") != 0) {
+  if (m != NULL && (PyModule_AddStringConstant(m, "SIGNATURE", "kvssd_hip_fused_decode/13") != 0 ||
+                    PyModule_AddStringConstant(m, "BUILD_ID", kBuildIdMarked + sizeof("kvssd-build-id:") - 1) != 0)) {
     Py_DECREF(m);
     return NULL;
   }

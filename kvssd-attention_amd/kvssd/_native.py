@@ -174,14 +174,17 @@ def fused_decode_fast():
     ``call(entry, desc, query, packed_k, packed_v, scales_k, scales_v,
     valid_tokens, block_table, out, lse, workspace, workspace_bytes, stream)``
     with every pointer an int (or None) and ``desc`` the address of a
-    DecodeDesc, returning the status.  None when that module is absent or of
-    another signature (callers then use the ctypes function)."""
+    DecodeDesc, returning the status.  None when that module is absent, of
+    another signature or, beside the in-tree library, from other sources than
+    the library (callers then use the ctypes function)."""
     lib = load()
     try:
         from . import _fastcall
     except ImportError:
         return None
     if getattr(_fastcall, "SIGNATURE", None) != FASTCALL_SIGNATURE:
+        return None
+    if not LIB_PATH_OVERRIDDEN and getattr(_fastcall, "BUILD_ID", None) != lib.kvssd_hip_build_id().decode():
         return None
     return _fastcall.fused_decode, ctypes.cast(lib.kvssd_hip_fused_decode, ctypes.c_void_p).value
 

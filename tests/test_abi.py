@@ -273,3 +273,19 @@ def test_fast_call_module_matches_the_ctypes_call():
     assert "at least one block is required" in both(desc, None, fake, fake, fake, fake, 1)  # table
     with pytest.raises(TypeError, match="14 arguments"):
         call(entry, ctypes.addressof(desc))
+
+
+def test_fast_call_module_carries_the_build_id(monkeypatch):
+    # built from the same sources as the library (the id is also in the file,
+    # where the build script reads it), and refused when it is not
+    from kvssd import _fastcall
+
+    mod = _native.build_module()
+    tree = mod.source_hash()
+    assert _fastcall.BUILD_ID == _native.build_id() == tree == mod.built_id(mod.FASTCALL_OUT)
+    assert _native.fused_decode_fast() is not None
+    monkeypatch.setattr(_fastcall, "BUILD_ID", "0" * len(tree))
+    assert _native.fused_decode_fast() is None
+    monkeypatch.undo()
+    monkeypatch.setattr(_fastcall, "SIGNATURE", "kvssd_hip_fused_decode/12")
+    assert _native.fused_decode_fast() is None
