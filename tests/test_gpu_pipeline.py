@@ -94,6 +94,47 @@ def test_resident_decode_over_many_selections(cuda_device, tmp_path: Path):
         assert len(pipe._resident[0].tables) <= 8
 
 
+def test_resident_whole_layer_alternating_queries(cuda_device, tmp_path: Path):
+    """Whole-layer decodes of a resident layer re-enter the last call's prepared
+    decode only for a query of its shape, dtype and device: queries that change
+    dtype, sit on the host, are strided views or have fewer heads each take a
+    prepared decode of their own, and every result (kept across later calls)
+    matches the oracle in the query's dtype."""
+    store, (pk, pv, sk, sv, valid) = build_store(tmp_path, 2500, 4)  # 20 blocks, last one partial
+    scale = 1 / math.sqrt(128)
+    base = torch.randn(32, 128, generator=torch.Generator().manual_seed(11))
+    wide = torch.randn(32, 256, generator=torch.Generator().manual_seed(12))
+    queries = [
+        base.half().to(cuda_device),
+        base.to(cuda_device),
+        base.half(),  # host tensor: copied to the device by the pipeline
+        base.bfloat16().to(cuda_device),
+        wide.half().to(cuda_device)[:, ::2],  # strided view of the same values as below
+        wide[:, ::2].contiguous().half().to(cuda_device),
+        base[:16].half().to(cuda_device),  # fewer query heads: GQA group of 2
+        base.half().to(cuda_device),
+    ]
+    outs = []
+    with KVSSDPipeline(store, device=cuda_device, attention_backend="hip") as pipe:
+        pipe.load_resident([0])
+        for _ in range(2):
+            for q in queries:
+                outs.append((q, pipe.decode(q, 0)))
+        res = pipe._resident[0]
+        assert res.whole is not None and res.whole.matches(queries[-1])
+        torch.cuda.synchronize()
+    for q, out in outs:
+        assert out.dtype == q.dtype and out.device.type == "cuda" and out.shape == q.shape
+        ref, _ = O.attention(q.float().cpu().numpy(), pk, pv, sk, sv, valid, 4, 32, scale)
+        np.testing.assert_allclose(out.float().cpu().numpy(), ref, atol=ATOL, rtol=RTOL)
+    # the repeated queries (same values, every call its own output tensor) agree exactly
+    n = len(queries)
+    for i in range(n):
+        assert outs[i][1].data_ptr() != outs[n + i][1].data_ptr()
+        assert torch.equal(outs[i][1], outs[n + i][1])
+    assert torch.equal(outs[4][1], outs[5][1])
+
+
 def test_require_cuda_kernel_runs_hip(cuda_device, tmp_path: Path):
     store, _ = build_store(tmp_path, 300, 4)
     with KVSSDPipeline(store, device=cuda_device, require_cuda_kernel=True) as pipe:
