@@ -8,7 +8,8 @@
 //
 // Work split.  A workgroup of 8 waves owns KG consecutive kv heads (a
 // "group": 4, or 8 when kv_heads % 8 == 0 and the context is long enough to
-// fill the chip) and one split (a range of attended blocks).  It walks the
+// fill the chip) and one split (its share of the attended blocks: every
+// splits-th one for INT4, a contiguous run for INT2).  It walks the
 // split in stages of 512 / KG tokens (128 or 64); wave (w, half) computes kv
 // head w of the group over tokens 64*half .. 64*half+63 of every stage.  With
 // KG = 4 the two halves meet in LDS at the end; with KG = 8 there is one half.
@@ -112,9 +113,24 @@ struct StagedParams {
   const int32_t* table;
   float* part_o;
   float* part_ml;
-  int query_heads, kv_heads, block_tokens, num_blocks, units, blocks_per_split, gq;
+  int query_heads, kv_heads, block_tokens, num_blocks, units;
+  int split_arg;  // the number of splits (interleaved split order) or blocks per split (contiguous)
+  int gq;
   float scale_log2;  // sm_scale * log2(e)
 };
+
+// Which units a split attends.  Interleaved: split s takes units s, s + splits,
+// s + 2 splits, ..., so at any moment the workgroups stream neighbouring
+// blocks and a stage round's reads fall on every HBM channel evenly.  With a
+// contiguous run of blocks per split the workgroups' streams sit a fixed
+// power-of-two distance apart: a plain read of the INT4 128K layer in this
+// kernel's stage pattern (256 workgroups, 64-token stages of K, V and scales)
+// took 29.1 us that way against 25.7 us interleaved, and the INT4 128K split
+// kernel went 28.6 -> 27.0 us, 1M 171.2 -> 169.7 us.  INT2's stage round is
+// bound by its math, not by its reads; it measured 0.1 us slower interleaved
+// (128K) and keeps the contiguous runs.
+template <int BITS>
+constexpr bool kInterleavedSplits = BITS == 4;
 
 // XOR swizzle of a region's chunk index for token t (CPT chunks per token).
 // A token row of 16 or more chunks spans every bank group, so the swizzle
@@ -447,8 +463,7 @@ template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
 __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* query, const uint8_t* pk,
                                                                  const uint8_t* pv, const uint8_t* sk,
                                                                  const uint8_t* sv, uint32_t heads, int block_tokens,
-                                                                 int blocks_per_split, int units_total,
-                                                                 DecodeTail r) {
+                                                                 int split_arg, int units_total, DecodeTail r) {
   const StagedParams p{query,           pk,
                        pv,              sk,
                        sv,              r.valid,
@@ -456,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
                        r.part_ml,       r.query_heads,
                        static_cast<int>(heads & 0xFFFFu), block_tokens,
                        r.num_blocks,    units_total,
-                       blocks_per_split, static_cast<int>((heads >> 16) & 0xFFu),
+                       split_arg,       static_cast<int>((heads >> 16) & 0xFFu),
                        r.scale_log2};
   const bool has_table = (heads & kHasTable) != 0;
   // the non-preloaded arguments, in SGPRs from here on (they stay live, so no
@@ -487,17 +502,22 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
   const int rest = blockIdx.x >> 3;
   const int grp = rest % groups;
   const int split = (rest / groups) * 8 + xcd;
-  const int u_begin = split * p.blocks_per_split;
-  // padding ids of the last round (splits = ceil(units / blocks_per_split))
-  if (u_begin >= p.units) return;
-  const int u_end = min(p.units, u_begin + p.blocks_per_split);
+  // the split's units: u_first, u_first + u_stride, ... (n_units of them)
+  constexpr bool kInterleave = kInterleavedSplits<BITS>;
+  const int u_first = kInterleave ? split : split * p.split_arg;
+  const int u_stride = kInterleave ? p.split_arg : 1;
+  // padding ids of the last round (splits = ceil(units / blocks per split))
+  if (kInterleave ? split >= p.split_arg : u_first >= p.units) return;
+  const int u_end = kInterleave ? p.units : min(p.units, u_first + p.split_arg);  // contiguous: the run's end
   const int kvh0 = grp * KG;
   const int head0 = (kvh0 + w) * p.gq;
 
   const CopyMap<BITS, KG> cm = make_copy_map<BITS, KG>(wave, lane, p.kv_heads);
   const uint32_t lds0 = lds_addr(lds);
   int* units = reinterpret_cast<int*>(lds + 2 * G::STAGE + kWBytes);
-  const int n_units = max(0, u_end - u_begin);  // <= kMaxUnits, checked on the host
+  // At least one (splits <= units); at most blocks per split <= kMaxUnits,
+  // checked on the host (interleaved: ceil(units / splits) <= blocks per split).
+  const int n_units = kInterleave ? (p.units - 1 - split) / u_stride + 1 : max(0, u_end - u_first);
 
   // Early form (no block table, the query 16-byte aligned, and room in the
   // second stage buffer for the query scratch and the workgroup's query
@@ -512,7 +532,7 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
   constexpr bool kEarlyFits = kWaves * coop_scratch_bytes<QUADS> + kQBytesMax <= G::STAGE;
   const bool direct = kEarlyFits && !has_table && (reinterpret_cast<uintptr_t>(p.query) & 15u) == 0;
   auto advance = [&](Cursor& c) -> bool {
-    return direct ? next_stage_direct<kStage>(c, units, u_begin, p.block_tokens, n_units)
+    return direct ? next_stage_direct<kStage>(c, units, u_first, u_stride, p.block_tokens, n_units)
                   : next_stage<kStage>(c, units, n_units);
   };
 
@@ -532,18 +552,18 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
       dma16<false>(qsrc, 1024u * static_cast<uint32_t>(i) + 16u * static_cast<uint32_t>(lane),
                    lds_addr(qrows) + 1024u * static_cast<uint32_t>(i));
     if (n_units > 0) {
-      issue_stage<BITS, KG>(p, lds0, Cursor{0, u_begin, 0, 0}, kvh0, wave, cm);
+      issue_stage<BITS, KG>(p, lds0, Cursor{0, u_first, 0, 0}, kvh0, wave, cm);
       spec = true;
     }
     rest_in_sgprs();
     // the split's valid counts, 64 per copy (lanes past the end re-read the
     // last one): the only early copies whose address is not preloaded, so
     // they go last; they are first read once stage 0 has landed
-    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(p.valid + (n_units > 0 ? u_begin : 0));
+    const uint8_t* vsrc = reinterpret_cast<const uint8_t*>(p.valid + (n_units > 0 ? u_first : 0));
     const int ulast = max(n_units - 1, 0);
     int vcopies = 0;
     for (int i0 = 64 * wave; i0 < n_units; i0 += 64 * kWaves, ++vcopies)
-      dma4(vsrc, 4u * static_cast<uint32_t>(min(i0 + lane, ulast)),
+      dma4(vsrc, 4u * static_cast<uint32_t>(min(i0 + lane, ulast) * u_stride),
            lds_addr(reinterpret_cast<const uint8_t*>(units)) + 4u * static_cast<uint32_t>(i0));
     KVSSD_STAMP(kStampStage0Issued);
     // the query rows (issued first) have landed once at most the stage's
@@ -560,10 +580,10 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
     bool issued1 = false;
     if (spec) {
       if (p.block_tokens > kStage) {
-        c1 = Cursor{0, u_begin, 0, kStage};
+        c1 = Cursor{0, u_first, 0, kStage};
         issued1 = true;
       } else if (n_units > 1) {
-        c1 = Cursor{1, u_begin + 1, 0, 0};
+        c1 = Cursor{1, u_first + u_stride, 0, 0};
         issued1 = true;
       }
       if (issued1) issue_stage<BITS, KG>(p, lds0 + static_cast<uint32_t>(G::STAGE), c1, kvh0, wave, cm);
@@ -592,8 +612,8 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
     // attended block, its first stage of tokens (one scalar read with a block
     // table).  If that block holds no valid token they are simply not used.
     rest_in_sgprs();
-    if (u_begin < u_end) {
-      Cursor c0{0, __builtin_amdgcn_readfirstlane(p.table ? p.table[u_begin] : u_begin), 0, 0};
+    if (n_units > 0) {
+      Cursor c0{0, __builtin_amdgcn_readfirstlane(p.table ? p.table[u_first] : u_first), 0, 0};
       if (c0.blk >= 0 && c0.blk < p.num_blocks) {
         issue_stage<BITS, KG>(p, lds0, c0, kvh0, wave, cm);
         spec = true;
@@ -604,7 +624,8 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
     const QueryRaw<QUADS> qraw = coop_query_load<BITS, QUADS, QT>(p.query, p.gq, head0, lane);
     // the split's (block id, clamped valid count) list, read once into LDS
     for (int i = threadIdx.x; i < n_units; i += kThreads) {
-      const int blk = p.table ? p.table[u_begin + i] : u_begin + i;
+      const int ui = u_first + i * u_stride;
+      const int blk = p.table ? p.table[ui] : ui;
       units[2 * i] = blk;
       units[2 * i + 1] = (blk < 0 || blk >= p.num_blocks) ? 0 : clamp_valid(p.valid[blk], p.block_tokens);
     }
@@ -792,29 +813,30 @@ __global__ __launch_bounds__(kThreads) void decode_staged_kernel(const void* que
 }
 
 template <int BITS, int QUADS, int QSPLIT, typename QT, int KG>
-void launch_one(const StagedParams& prm, int splits, int grid, hipStream_t s) {
+void launch_one(const StagedParams& prm, const SplitPlan& plan, int grid, hipStream_t s) {
   const uint32_t heads = pack_heads(prm.kv_heads, prm.gq, prm.table != nullptr);
   const DecodeTail rest{prm.valid,       prm.table,        prm.part_o,     prm.part_ml,
-                        prm.query_heads, prm.num_blocks,   prm.scale_log2, splits};
+                        prm.query_heads, prm.num_blocks,   prm.scale_log2, plan.splits};
+  const int split_arg = kInterleavedSplits<BITS> ? plan.splits : plan.blocks_per_split;
   hipLaunchKernelGGL((decode_staged_kernel<BITS, QUADS, QSPLIT, QT, KG>), dim3(grid), dim3(kThreads), 0, s, prm.query,
-                     prm.pk, prm.pv, prm.sk, prm.sv, heads, prm.block_tokens, prm.blocks_per_split, prm.units, rest);
+                     prm.pk, prm.pv, prm.sk, prm.sv, heads, prm.block_tokens, split_arg, prm.units, rest);
 }
 
 template <int BITS, int QUADS, int KG>
-int launch_quads(const StagedParams& prm, int splits, int grid, int dtype, hipStream_t s) {
+int launch_quads(const StagedParams& prm, const SplitPlan& plan, int grid, int dtype, hipStream_t s) {
   switch (dtype) {
     case KVSSD_DTYPE_F16:
-      launch_one<BITS, QUADS, 1, _Float16, KG>(prm, splits, grid, s);
+      launch_one<BITS, QUADS, 1, _Float16, KG>(prm, plan, grid, s);
       break;
     case KVSSD_DTYPE_BF16:  // 8 significant bits: one fp16 part holds a normalised value exactly
-      launch_one<BITS, QUADS, 1, uint16_t, KG>(prm, splits, grid, s);
+      launch_one<BITS, QUADS, 1, uint16_t, KG>(prm, plan, grid, s);
       break;
     case KVSSD_DTYPE_F32:
     case KVSSD_DTYPE_F64:
       // (staged_wide never picks 8 kv heads for INT4 with two quads here)
       if constexpr (BITS == 4 && QUADS == 2 && KG == 8) return arg_error("no 8-kv-head form for this query");
-      else if (dtype == KVSSD_DTYPE_F32) launch_one<BITS, QUADS, 2, float, KG>(prm, splits, grid, s);
-      else launch_one<BITS, QUADS, 2, double, KG>(prm, splits, grid, s);
+      else if (dtype == KVSSD_DTYPE_F32) launch_one<BITS, QUADS, 2, float, KG>(prm, plan, grid, s);
+      else launch_one<BITS, QUADS, 2, double, KG>(prm, plan, grid, s);
       break;
     default:
       return arg_error("unsupported query dtype");
@@ -823,12 +845,12 @@ int launch_quads(const StagedParams& prm, int splits, int grid, int dtype, hipSt
 }
 
 template <int KG>
-int launch_kg(const StagedParams& prm, int splits, int bits, int dtype, hipStream_t s) {
-  const int grid = 8 * (prm.kv_heads / KG) * ((splits + 7) / 8);
+int launch_kg(const StagedParams& prm, const SplitPlan& plan, int bits, int dtype, hipStream_t s) {
+  const int grid = 8 * (prm.kv_heads / KG) * ((plan.splits + 7) / 8);
   const bool two = prm.gq > 4;
   if (bits == 4)
-    return two ? launch_quads<4, 2, KG>(prm, splits, grid, dtype, s) : launch_quads<4, 1, KG>(prm, splits, grid, dtype, s);
-  return two ? launch_quads<2, 2, KG>(prm, splits, grid, dtype, s) : launch_quads<2, 1, KG>(prm, splits, grid, dtype, s);
+    return two ? launch_quads<4, 2, KG>(prm, plan, grid, dtype, s) : launch_quads<4, 1, KG>(prm, plan, grid, dtype, s);
+  return two ? launch_quads<2, 2, KG>(prm, plan, grid, dtype, s) : launch_quads<2, 1, KG>(prm, plan, grid, dtype, s);
 }
 
 }  // namespace
@@ -885,11 +907,10 @@ int launch_staged(const DecodeArgs& a, const SplitPlan& plan, SplitPartials part
   prm.block_tokens = d.block_tokens;
   prm.num_blocks = d.num_blocks;
   prm.units = a.units;
-  prm.blocks_per_split = plan.blocks_per_split;
   prm.gq = d.query_heads / d.kv_heads;
   prm.scale_log2 = static_cast<float>(d.sm_scale) * kLog2e;
-  if (staged_wide(d, a.units)) return launch_kg<8>(prm, plan.splits, d.bits, d.query_dtype, a.stream);
-  return launch_kg<4>(prm, plan.splits, d.bits, d.query_dtype, a.stream);
+  if (staged_wide(d, a.units)) return launch_kg<8>(prm, plan, d.bits, d.query_dtype, a.stream);
+  return launch_kg<4>(prm, plan, d.bits, d.query_dtype, a.stream);
 }
 
 }  // namespace kvssd

@@ -263,15 +263,15 @@ __device__ __forceinline__ bool next_stage(Cursor& c, const int* units, int n_un
 }
 
 // As next_stage for a split without a block table: unit u is block
-// u_begin + u and vraw[u] its raw valid count (LDS, copied straight from the
-// valid array), clamped here.
+// first + u * stride and vraw[u] its raw valid count (LDS, copied straight
+// from the valid array), clamped here.
 template <int STAGE_TOK>
-__device__ __forceinline__ bool next_stage_direct(Cursor& c, const int* vraw, int u_begin, int block_tokens,
-                                                  int n_units) {
+__device__ __forceinline__ bool next_stage_direct(Cursor& c, const int* vraw, int first, int stride,
+                                                  int block_tokens, int n_units) {
   c.sb0 += STAGE_TOK;
   while (c.sb0 >= c.vb) {
     if (++c.u >= n_units) return false;
-    c.blk = u_begin + c.u;
+    c.blk = first + c.u * stride;
     c.vb = __builtin_amdgcn_readfirstlane(clamp_valid(vraw[c.u], block_tokens));
     c.sb0 = 0;
   }
