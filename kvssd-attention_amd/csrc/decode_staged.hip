@@ -454,8 +454,9 @@ __device__ __forceinline__ void wait_copies_left(int extra) {
 // offset plus a constant the LDS instructions take as their immediate offset
 // (a runtime buffer costs ~10 address adds per wave and stage): the INT2 128K
 // GQA-4 step 23.5-23.6 -> 23.25-23.3 us (two rounds of three A/B pairs, one
-// box each), GQA 8 unchanged.  INT4 measured no faster with it (128K +0.15 us)
-// and keeps the loop below; the two-quad fp32 / fp64 INT2 form would spill.
+// box each), GQA 8 unchanged.  INT4 measured no faster with it (128K within
+// +-0.15 us, 256K and 1M within 1 us either way, A/B pairs) and keeps the loop
+// below; the two-quad fp32 / fp64 INT2 form would spill.
 template <int BITS, int QUADS, int QSPLIT>
 constexpr bool kUnrollByBuffer = BITS == 2 && !(QUADS == 2 && QSPLIT == 2);
 
