@@ -121,14 +121,14 @@ struct StagedParams {
 
 // Which units a split attends.  Interleaved: split s takes units s, s + splits,
 // s + 2 splits, ..., so at any moment the workgroups stream neighbouring
-// blocks and a stage round's reads fall on every HBM channel evenly.  With a
-// contiguous run of blocks per split the workgroups' streams sit a fixed
-// power-of-two distance apart: a plain read of the INT4 128K layer in this
-// kernel's stage pattern (256 workgroups, 64-token stages of K, V and scales)
+// blocks.  With a contiguous run of blocks per split their streams sit a fixed
+// power-of-two distance apart (256 KB of K codes at 128K), and HBM serves that
+// pattern slower: a plain read of the INT4 128K layer in this kernel's stage
+// pattern (256 workgroups, 64-token stages of K, V and scales, plain loads)
 // took 29.1 us that way against 25.7 us interleaved, and the INT4 128K split
-// kernel went 28.6 -> 27.0 us, 1M 171.2 -> 169.7 us.  INT2's stage round is
-// bound by its math, not by its reads; it measured 0.1 us slower interleaved
-// (128K) and keeps the contiguous runs.
+// kernel went 28.5-28.8 -> 27.0-27.2 us (A/B pairs; 1M 0.2-1.5 us faster).
+// INT2's stage round is bound by its math, not by its reads; it measured
+// 0.1 us slower interleaved (128K) and keeps the contiguous runs.
 template <int BITS>
 constexpr bool kInterleavedSplits = BITS == 4;
 
