@@ -67,8 +67,13 @@ WORKLOAD_LABELS = {
     "int2_gqa_128k": "INT2 GQA 128K tokens",
     "int4_gqa_4k": "INT4 GQA 4K tokens",
     "int4_gqa8_256k_sparse": "INT4 GQA 8, 256K tokens, RecentSinkBlocks(1, 32)",
+    "int4_gqa_16k": "INT4 GQA 16K tokens",
+    "int4_gqa_32k": "INT4 GQA 32K tokens",
+    "int4_gqa_64k": "INT4 GQA 64K tokens",
     "int4_gqa_256k": "INT4 GQA 256K tokens",
+    "int4_gqa_512k": "INT4 GQA 512K tokens (HBM-resident)",
     "int4_gqa_1m": "INT4 GQA 1M tokens (HBM-resident)",
+    "int4_gqa_2m": "INT4 GQA 2M tokens (HBM-resident)",
 }
 HBM_PEAK_GBPS = 8000.0
 
@@ -78,9 +83,14 @@ WORKLOADS = {
     "int4_gqa_128k": (131072, 4, 32, 0.5, 0.0, None),
     "int2_gqa_128k": (131072, 2, 32, 1.0, 0.05, None),
     "int4_gqa8_256k_sparse": (262144, 4, 64, 1.0, 0.0, (1, 32)),
-    # longer contexts of the same shape, resident in HBM (context-length scaling)
+    # other context lengths of the same shape, resident in HBM (context-length scaling)
+    "int4_gqa_16k": (16384, 4, 32, 0.5, 0.0, None),
+    "int4_gqa_32k": (32768, 4, 32, 0.5, 0.0, None),
+    "int4_gqa_64k": (65536, 4, 32, 0.5, 0.0, None),
     "int4_gqa_256k": (262144, 4, 32, 0.5, 0.0, None),
+    "int4_gqa_512k": (524288, 4, 32, 0.5, 0.0, None),
     "int4_gqa_1m": (1048576, 4, 32, 0.5, 0.0, None),
+    "int4_gqa_2m": (2097152, 4, 32, 0.5, 0.0, None),
 }
 # name -> (tokens, bits, query_heads, stage_blocks): records in page-locked host memory
 HOST_STAGED = {

@@ -23,7 +23,7 @@ def test_help_names_the_workloads_and_the_warmup_and_settle_defaults():
     assert proc.returncode == 0
     for name in (
         "int4_gqa_128k", "int2_gqa_128k", "int4_gqa_4k", "int4_gqa8_256k_sparse", "int4_gqa_256k", "int4_gqa_1m",
-        "int4_gqa_1m_host_staged",
+        "int4_gqa_16k", "int4_gqa_32k", "int4_gqa_64k", "int4_gqa_512k", "int4_gqa_2m", "int4_gqa_1m_host_staged",
     ):
         assert name in proc.stdout
     text = " ".join(proc.stdout.split())
